@@ -1,0 +1,78 @@
+"""Builds libpa_decode.so (the C ABI in include/pa_decode.h) for gfx950.
+
+    python paged-attention_amd/build.py          # compile + link in-tree
+
+The library is written to paged-attention_amd/lib/ so that it travels with the
+source tree; nothing is installed. Every call recompiles (a few seconds per
+file), so the result always matches the sources.
+"""
+
+from __future__ import annotations
+
+import os
+import pathlib
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+
+PKG = pathlib.Path(__file__).resolve().parent
+ROOT = PKG.parent
+CSRC = PKG / "csrc"
+LIB_DIR = PKG / "lib"
+OBJ_DIR = PKG / "_build"
+LIB = LIB_DIR / "libpa_decode.so"
+
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+ARCH = "gfx950"
+
+# Packed-FP32 VALU ops are disabled on purpose (they have produced silent wrong
+# results on this hardware pool); the host pass warns that it does not know the
+# feature, which is harmless.
+COMMON = [
+    "-O3",
+    "-std=c++20",
+    "-fPIC",
+    f"--offload-arch={ARCH}",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall",
+    "-Wno-unused-command-line-argument",
+    f"-I{ROOT / 'include'}",
+    f"-I{CSRC}",
+]
+
+SOURCES = ["pa_kernels.hip", "pa_capi.cpp"]
+
+
+def _run(cmd: list[str]) -> None:
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        sys.stderr.write(proc.stdout + proc.stderr)
+        raise RuntimeError(f"command failed ({proc.returncode}): {' '.join(cmd)}")
+
+
+def build(verbose: bool = False) -> pathlib.Path:
+    OBJ_DIR.mkdir(exist_ok=True)
+    LIB_DIR.mkdir(exist_ok=True)
+    jobs = []
+    objs = []
+    for src in SOURCES:
+        obj = OBJ_DIR / (src + ".o")
+        lang = ["-x", "hip"] if src.endswith(".hip") else []
+        jobs.append([HIPCC, *COMMON, *lang, "-c", str(CSRC / src), "-o", str(obj)])
+        objs.append(obj)
+    with ThreadPoolExecutor(max_workers=len(jobs)) as ex:
+        for cmd in jobs:
+            if verbose:
+                print(" ".join(cmd), flush=True)
+        list(ex.map(_run, jobs))
+    tmp = LIB.with_suffix(".so.tmp")
+    link = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
+    if verbose:
+        print(" ".join(link), flush=True)
+    _run(link)
+    os.replace(tmp, LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    print(build(verbose="-v" in sys.argv))

@@ -1,0 +1,47 @@
+// Internal interface between the C-ABI host layer (pa_capi.cpp) and the
+// gfx950 kernels (pa_kernels.hip). Not installed; callers use pa_decode.h.
+#pragma once
+
+#include "pa_decode.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+
+namespace pa {
+
+// Raised by host code for a failed HIP runtime call; the C ABI maps it to
+// PA_ERR_DEVICE.
+struct DeviceError : std::runtime_error {
+    using std::runtime_error::runtime_error;
+};
+
+inline void hip_check(hipError_t e, const char* what) {
+    if (e != hipSuccess)
+        throw DeviceError(std::string(what) + ": " + hipGetErrorName(e) + " (" + hipGetErrorString(e) + ")");
+}
+
+constexpr int kHeadDim     = 128;   // the only head_dim the path supports (decode.cu:31-38)
+constexpr int kGroupTokens = 16;    // tokens per MFMA step of the decode kernel
+
+// Tokens per planning tile (decode.cu:43-45 tile_tokens). The gfx950 kernel
+// consumes 16-token groups, so every 16-token boundary is a legal cut.
+int kernel_tile_tokens(int dtype, int group);
+// Decode work units (waves) resident per CU at the kernel's occupancy.
+int kernel_units_per_cu(int dtype, int group);
+
+// Throws std::invalid_argument for unsupported (dtype, head_dim, group);
+// returns the launch status otherwise.
+hipError_t launch_decode_split(int dtype, const pa_decode_params& p, hipStream_t s);
+hipError_t launch_decode_merge(int dtype, const pa_decode_params& p, hipStream_t s);
+hipError_t launch_append(int dtype, const uint16_t* k, const uint16_t* v, void* k_cache,
+                         void* v_cache, const int32_t* bt_row, int start_pos, int n, int hkv,
+                         int page_size, float inv_k, float inv_v, hipStream_t s);
+hipError_t launch_gather(int dtype, const void* cache, const int32_t* bt_row, int hkv,
+                         int page_size, int kv_head, int len, void* out, hipStream_t s);
+hipError_t launch_stream_read(const void* buf, size_t bytes, int blocks, uint32_t* sink,
+                              hipStream_t s);
+
+}  // namespace pa

@@ -1,0 +1,84 @@
+"""The torch binding's `Decoder` (bindings/torch_decode.cu:14-81), same signature:
+
+    dec = Decoder(num_q_heads, num_kv_heads, head_dim, page_size, fp8)
+    dec.plan(seq_lens_cpu_int32, num_ctas=0)
+    out = dec.run(q, k_cache, v_cache, block_table, seq_lens_dev, k_scale, v_scale)
+    dec.num_ctas, dec.num_segments
+
+It runs libpa_decode.so's HIP kernels on the current torch stream. Argument
+checks raise RuntimeError, as TORCH_CHECK does in the reference.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import core
+from ._lib import DecodeParams
+
+
+def _require(cond: bool, msg: str = "Expected condition to hold") -> None:
+    if not cond:
+        raise RuntimeError(msg)
+
+
+class Decoder:
+    def __init__(self, num_q_heads: int, num_kv_heads: int, head_dim: int, page_size: int, fp8: bool):
+        self._hq = int(num_q_heads)
+        self._hkv = int(num_kv_heads)
+        self._dim = int(head_dim)
+        self._page = int(page_size)
+        self._dtype = core.FP8_E4M3 if fp8 else core.FP16
+        self._batch = 0
+        self._plan: core.DecodePlan | None = None
+        self._device_plan = core.DevicePlan()
+
+    # torch_decode.cu:21-27
+    def plan(self, seq_lens: torch.Tensor, num_ctas: int = 0) -> None:
+        _require(seq_lens.device.type == "cpu" and seq_lens.dtype == torch.int32,
+                 "seq_lens must be a CPU int32 tensor")
+        lens = seq_lens.contiguous().numpy()
+        self._plan = core.make_plan(self._dtype, lens, self._hq, self._hkv, self._dim, num_ctas)
+        self._device_plan.upload(self._plan, self._hq // self._hkv, self._dim,
+                                 torch.cuda.current_stream())
+        self._batch = int(lens.shape[0])
+
+    # torch_decode.cu:31-59
+    def run(self, q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+            block_table: torch.Tensor, seq_lens_dev: torch.Tensor, k_scale: float,
+            v_scale: float) -> torch.Tensor:
+        _require(q.is_cuda and q.dtype == torch.float16 and q.is_contiguous(),
+                 "q must be a contiguous CUDA fp16 tensor")
+        _require(k_cache.is_contiguous() and v_cache.is_contiguous() and block_table.is_contiguous(),
+                 "caches and block_table must be contiguous")
+        _require(q.size(0) == self._batch, "q batch does not match the plan")
+        _require(block_table.dtype == torch.int32, "block_table must be int32")
+        out = torch.empty_like(q)
+        p = DecodeParams()
+        p.q = q.data_ptr()
+        p.out = out.data_ptr()
+        p.k_cache = k_cache.data_ptr()
+        p.v_cache = v_cache.data_ptr()
+        p.block_table = block_table.data_ptr()
+        p.seq_lens = seq_lens_dev.data_ptr()
+        p.slot_ids = None
+        p.block_table_stride = int(block_table.size(1))
+        p.batch = self._batch
+        p.num_q_heads = self._hq
+        p.num_kv_heads = self._hkv
+        p.head_dim = self._dim
+        p.page_size = self._page
+        p.sm_scale = core.sm_scale(self._dim)
+        p.k_scale = float(k_scale)
+        p.v_scale = float(v_scale)
+        self._device_plan.bind(p)
+        core.paged_decode(self._dtype, p, torch.cuda.current_stream())
+        return out
+
+    @property
+    def num_ctas(self) -> int:
+        return self._plan.num_ctas if self._plan is not None else 0
+
+    @property
+    def num_segments(self) -> int:
+        return len(self._plan.segments) if self._plan is not None else 0

@@ -1,0 +1,79 @@
+"""The C ABI library (include/pa_decode.h): loads, exports every declared
+symbol, and maps errors to status codes without touching a device."""
+
+import ctypes
+import subprocess
+
+import pytest
+
+import pa_amd
+from pa_amd import _lib
+
+
+def test_library_exports_every_header_symbol():
+    lib = _lib.load()
+    declared = _lib.header_functions()
+    assert len(declared) >= 50
+    assert declared == sorted(_lib.SIGNATURES)
+    for name in declared:
+        assert hasattr(lib, name), name
+    out = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)], capture_output=True,
+                         text=True, check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if " T pa_" in line}
+    assert exported == set(declared)
+
+
+def test_library_has_gfx950_code_object():
+    data = _lib.LIB_PATH.read_bytes()
+    assert b"gfx950" in data
+
+
+def test_dtype_helpers():
+    assert pa_amd.kv_dtype_bytes(pa_amd.FP16) == 2 and pa_amd.kv_dtype_bytes(pa_amd.FP8_E4M3) == 1
+    assert pa_amd.kv_dtype_name(pa_amd.FP16) == "fp16"
+    assert pa_amd.kv_dtype_name(pa_amd.FP8_E4M3) == "fp8_e4m3"
+
+
+def test_tile_tokens_and_shape_errors():
+    for g in (1, 2, 4, 8):
+        assert pa_amd.tile_tokens(pa_amd.FP16, 128, g) == 16
+    out = ctypes.c_int()
+    lib = _lib.load()
+    assert lib.pa_tile_tokens(0, 64, 4, ctypes.byref(out)) == _lib.PA_ERR_INVALID_ARGUMENT
+    assert b"head_dim" in lib.pa_last_error()
+    assert lib.pa_tile_tokens(0, 128, 3, ctypes.byref(out)) == _lib.PA_ERR_INVALID_ARGUMENT
+    assert lib.pa_tile_tokens(7, 128, 4, ctypes.byref(out)) == _lib.PA_ERR_INVALID_ARGUMENT
+
+
+def test_decode_rejects_bad_shapes_before_any_launch():
+    p = _lib.DecodeParams()
+    p.num_q_heads, p.num_kv_heads, p.head_dim, p.num_ctas = 32, 8, 64, 4
+    with pytest.raises(pa_amd.InvalidArgument, match="head_dim"):
+        pa_amd.paged_decode(pa_amd.FP16, p, 0)
+    p.head_dim, p.num_q_heads = 128, 24
+    with pytest.raises(pa_amd.InvalidArgument, match="group"):
+        pa_amd.decode_split(pa_amd.FP16, p, 0)
+    p.num_q_heads = 32
+    with pytest.raises(pa_amd.InvalidArgument):
+        pa_amd.decode_split(pa_amd.FP16, p, 0)          # null pointers, page_size 0
+    lib = _lib.load()
+    assert lib.pa_decode(0, None, None) == _lib.PA_ERR_INVALID_ARGUMENT
+
+
+def test_null_handles_are_rejected():
+    lib = _lib.load()
+    assert lib.pa_plan_copy(None, None, None, None) == _lib.PA_ERR_INVALID_ARGUMENT
+    assert lib.pa_pool_release(None, 0) == _lib.PA_ERR_INVALID_ARGUMENT
+    assert lib.pa_cache_run(None, None, None, None) == _lib.PA_ERR_INVALID_ARGUMENT
+    assert lib.pa_pool_admit(None) == -1
+    assert lib.pa_append_quantize(0, None, None, None, None, None, 0, 4, 8, 128, 16, 1.0, 1.0, None) \
+        == _lib.PA_ERR_INVALID_ARGUMENT
+
+
+def test_device_queries_report_errors_not_crashes():
+    import torch
+    if torch.cuda.is_available():
+        assert pa_amd.wave_ctas(pa_amd.FP16, 128, 4) > 0
+    else:
+        with pytest.raises(pa_amd.DeviceError):
+            pa_amd.wave_ctas(pa_amd.FP16, 128, 4)

@@ -1,0 +1,242 @@
+"""GPU parity tests of the paged decode path, through the C ABI.
+
+Cases mirror tests/test_paged_decode.cu:158-221 of the reference (same shapes,
+lengths, page sizes, grids and chunked appends). The bar is tighter than the
+reference's 4e-3: max-abs <= 2e-3 against the fp32 CPU oracle (fp16 KV) or the
+oracle over the same dequantized FP8 values; stored cache bytes (block-table
+scatter and FP8 quantization) must be bit-exact.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+
+import oracle
+import pa_amd
+from helpers import D, TOL, d2h, normal_f16, run_cache_case, to_device
+
+pytestmark = pytest.mark.gpu
+
+DTYPES = [False, True]   # fp8?
+IDS = ["fp16", "fp8"]
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _device():
+    import torch
+    assert torch.cuda.is_available(), "GPU tests need a device"
+    pa_amd._lib.load()
+    yield
+
+
+@pytest.mark.parametrize("fp8", DTYPES, ids=IDS)
+def test_single_token_sequence(fp8):
+    err, _, _ = run_cache_case(fp8, 32, 8, 16, [1])
+    assert err < TOL, err
+
+
+@pytest.mark.parametrize("fp8", DTYPES, ids=IDS)
+@pytest.mark.parametrize("hq,hkv", [(8, 8), (8, 4), (16, 4), (32, 8), (8, 1)])
+def test_gqa_groups(fp8, hq, hkv):
+    err, _, _ = run_cache_case(fp8, hq, hkv, 16, [777])
+    assert err < TOL, err
+
+
+@pytest.mark.parametrize("fp8", DTYPES, ids=IDS)
+def test_mixed_length_batch(fp8):
+    err, _, _ = run_cache_case(fp8, 32, 8, 16, [1, 15, 16, 17, 129, 1000, 4099])
+    assert err < TOL, err
+
+
+@pytest.mark.parametrize("fp8", DTYPES, ids=IDS)
+@pytest.mark.parametrize("page_size", [1, 3, 8, 16, 32, 128])
+def test_page_sizes(fp8, page_size):
+    err, _, _ = run_cache_case(fp8, 16, 4, page_size, [300, 2500])
+    assert err < TOL, err
+
+
+@pytest.mark.parametrize("fp8", DTYPES, ids=IDS)
+@pytest.mark.parametrize("ctas", [1, 2, 7, 64, 1000])
+def test_forced_cta_counts(fp8, ctas):
+    err, _, plan = run_cache_case(fp8, 32, 8, 16, [5000, 90, 1, 700], num_ctas=ctas)
+    assert plan.num_ctas <= ctas
+    assert err < TOL, err
+
+
+@pytest.mark.parametrize("fp8", DTYPES, ids=IDS)
+def test_scattered_pages(fp8):
+    err, _, _ = run_cache_case(fp8, 32, 8, 16, [400, 333, 612], chunk=5, shuffle_seed=7)
+    assert err < TOL, err
+
+
+@pytest.mark.parametrize("fp8", DTYPES, ids=IDS)
+def test_long_sequence(fp8):
+    err, _, _ = run_cache_case(fp8, 32, 8, 16, [32768], threads=16)
+    assert err < TOL, err
+
+
+def test_fp8_quantization_error_is_small():
+    # tests/test_paged_decode.cu:200-204: against the unquantized fp16 values.
+    err, _, _ = run_cache_case(True, 32, 8, 16, [2048], quantized_reference=False)
+    assert err < 5e-2, err
+
+
+@pytest.mark.parametrize("fp8", DTYPES, ids=IDS)
+def test_output_invariant_under_page_placement(fp8):
+    """The plan and the arithmetic do not depend on where pages live: outputs
+    must be bitwise identical across page permutations and page sizes."""
+    lens = [700, 1, 2049, 64]
+    outs = []
+    for page_size, shuffle in [(16, None), (16, 3), (4, 11), (1, 5), (2048 + 64, None)]:
+        _, out, _ = run_cache_case(fp8, 32, 8, page_size, lens, shuffle_seed=shuffle)
+        outs.append(out)
+    for o in outs[1:]:
+        assert np.array_equal(o.view(np.uint32), outs[0].view(np.uint32))
+
+
+@pytest.mark.parametrize("scale", [1.0, 4.0 / 448.0, 2.0 / 448.0, 4.87 / 448.0, 0.5, 3.0, 1e-3])
+def test_append_fp8_bytes_exhaustive(scale):
+    """Every fp16 input (all 65536 bit patterns, NaN and infinity included)
+    through the append kernel, bit-exact against the oracle's E4M3 encoder."""
+    import torch
+    hkv, P = 1, 16
+    n = 65536 // D                                  # 512 tokens x 128 dims
+    k = np.arange(65536, dtype=np.uint16).reshape(n, hkv * D)
+    v = k[::-1].copy()
+    pages = n // P
+    table = np.random.default_rng(1).permutation(pages).astype(np.int32)
+    kc = torch.zeros(pages * hkv * P * D, dtype=torch.uint8, device="cuda")
+    vc = torch.zeros_like(kc)
+    inv = float(np.float32(1.0) / np.float32(scale))
+    pa_amd.append_quantize(pa_amd.FP8_E4M3, to_device(k), to_device(v), kc, vc, to_device(table), 0, n, hkv, D,
+                           P, inv, inv)
+    torch.cuda.synchronize()
+    ck = np.zeros(pages * P * D, dtype=np.uint8)
+    cv = np.zeros_like(ck)
+    oracle.append(1, k, v, ck, cv, table, 0, hkv, D, P, inv, inv)
+    assert np.array_equal(kc.cpu().numpy(), ck)
+    assert np.array_equal(vc.cpu().numpy(), cv)
+
+
+@pytest.mark.parametrize("fp8", DTYPES, ids=IDS)
+@pytest.mark.parametrize("page_size,start", [(1, 0), (3, 5), (16, 0), (16, 9), (64, 100)])
+def test_append_and_gather_bit_exact(fp8, page_size, start):
+    """Append at an offset into scattered pages, then read it back through the
+    decode kernel's own address function (gather probe); both bit-exact."""
+    import torch
+    dt = pa_amd.FP8_E4M3 if fp8 else pa_amd.FP16
+    hkv, n = 4, 333
+    rng = np.random.default_rng(page_size * 100 + start)
+    k = normal_f16(rng, (n, hkv * D))
+    v = normal_f16(rng, (n, hkv * D))
+    pages = math.ceil((start + n) / page_size)
+    pool_pages = pages + 7
+    table = rng.permutation(pool_pages)[:pages].astype(np.int32)
+    eb = 1 if fp8 else 2
+    nbytes = pool_pages * hkv * page_size * D * eb
+    kc = torch.zeros(nbytes, dtype=torch.uint8, device="cuda")
+    vc = torch.zeros_like(kc)
+    inv = float(np.float32(448.0 / 4.0))
+    pa_amd.append_quantize(dt, to_device(k), to_device(v), kc, vc, to_device(table), start, n, hkv, D, page_size,
+                           inv, inv)
+    ck = np.zeros(nbytes, dtype=np.uint8)
+    cv = np.zeros_like(ck)
+    view = (lambda a: a) if fp8 else (lambda a: a.view(np.uint16))
+    oracle.append(dt, k, v, view(ck), view(cv), table, start, hkv, D, page_size, inv, inv)
+    torch.cuda.synchronize()
+    assert np.array_equal(kc.cpu().numpy(), ck)
+    assert np.array_equal(vc.cpu().numpy(), cv)
+    length = start + n
+    dtable = to_device(table)
+    for h in range(hkv):
+        got = torch.zeros(length * D * eb, dtype=torch.uint8, device="cuda")
+        pa_amd.gather_kv(dt, kc, dtable, hkv, D, page_size, h, length, got)
+        torch.cuda.synchronize()
+        exp = oracle.gather_raw(dt, view(ck), table, hkv, D, page_size, h, length)
+        assert np.array_equal(got.cpu().numpy(), exp.view(np.uint8).reshape(-1))
+
+
+def _paged_inputs(batch, seq_lens, hq, hkv, page_size, fp8, seed):
+    """compare_flashinfer.py:80-97 style inputs: N(0,1) pools filled on the
+    device, a random page permutation as block table, per-tensor amax/448
+    scales with append-time quantization for FP8."""
+    import torch
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    pages_per = [math.ceil(L / page_size) for L in seq_lens]
+    num_pages = sum(pages_per)
+    max_pages = max(pages_per)
+    perm = torch.randperm(num_pages, device="cuda", generator=g).to(torch.int32)
+    table = torch.zeros(batch, max_pages, dtype=torch.int32, device="cuda")
+    off = 0
+    for b, n in enumerate(pages_per):
+        table[b, :n] = perm[off:off + n]
+        off += n
+    q = torch.randn(batch, hq, D, device="cuda", dtype=torch.float16, generator=g)
+    if not fp8:
+        k = torch.randn(num_pages, hkv, page_size, D, device="cuda", dtype=torch.float16, generator=g)
+        v = torch.randn(num_pages, hkv, page_size, D, device="cuda", dtype=torch.float16, generator=g)
+        return q, k, v, table, 1.0, 1.0
+    kc = torch.zeros(num_pages, hkv, page_size, D, device="cuda", dtype=torch.uint8)
+    vc = torch.zeros_like(kc)
+    srcs = []
+    for b, L in enumerate(seq_lens):
+        srcs.append((torch.randn(L, hkv, D, device="cuda", dtype=torch.float16, generator=g),
+                     torch.randn(L, hkv, D, device="cuda", dtype=torch.float16, generator=g)))
+    k_scale = max(float(s[0].abs().max()) for s in srcs) / 448.0
+    v_scale = max(float(s[1].abs().max()) for s in srcs) / 448.0
+    ik = float(np.float32(1.0) / np.float32(k_scale))
+    iv = float(np.float32(1.0) / np.float32(v_scale))
+    for b, (ks, vs) in enumerate(srcs):
+        pa_amd.append_quantize(pa_amd.FP8_E4M3, ks, vs, kc, vc, table[b], 0, seq_lens[b], hkv, D, page_size, ik, iv)
+    return q, kc, vc, table, k_scale, v_scale
+
+
+def _decoder_case(batch, seq_lens, fp8, page_size=16, hq=32, hkv=8, seed=0, threads=16):
+    import torch
+    q, k, v, table, ks, vs = _paged_inputs(batch, seq_lens, hq, hkv, page_size, fp8, seed)
+    dec = pa_amd.Decoder(hq, hkv, D, page_size, fp8)
+    lens = torch.tensor(seq_lens, dtype=torch.int32)
+    dec.plan(lens, 0)
+    out = dec.run(q, k, v, table, lens.cuda(), ks, vs)
+    torch.cuda.synchronize()
+    dt = pa_amd.FP8_E4M3 if fp8 else pa_amd.FP16
+    kb = k.view(torch.uint8).cpu().numpy() if fp8 else k.view(torch.int16).cpu().numpy().view(np.uint16)
+    vb = v.view(torch.uint8).cpu().numpy() if fp8 else v.view(torch.int16).cpu().numpy().view(np.uint16)
+    ref = oracle.paged_decode(dt, q.view(torch.int16).cpu().numpy().view(np.uint16), kb, vb,
+                              table.cpu().numpy(), np.asarray(seq_lens, np.int32), hq, hkv, D, page_size, ks, vs,
+                              threads=threads)
+    got = out.float().cpu().numpy()
+    return float(np.max(np.abs(got - ref))), dec
+
+
+@pytest.mark.parametrize("fp8", DTYPES, ids=IDS)
+def test_decoder_binding_config1(fp8):
+    """BASELINE config 1 shape (4 x 1024, P=16, scattered) via the torch_decode
+    `Decoder` signature."""
+    err, dec = _decoder_case(4, [1024] * 4, fp8)
+    assert dec.num_ctas > 0 and dec.num_segments >= 32
+    assert err < TOL, err
+
+
+def test_decoder_full_size_config2():
+    """BASELINE config 2 at full size: 32 x 8192 fp16, 16-token scattered pages."""
+    err, _ = _decoder_case(32, [8192] * 32, False, threads=16)
+    assert err < TOL, err
+
+
+def test_decoder_long_context_config5_fp8():
+    """BASELINE config 5 (1 x 131072), FP8 KV: hundreds of splits per row."""
+    err, dec = _decoder_case(1, [131072], True, threads=8)
+    assert dec.num_segments > 8 * 64
+    assert err < TOL, err
+
+
+def test_decoder_ragged_config4_subset():
+    """BASELINE config 4's ragged lengths (U[128, 16384] from a seed), first 16 rows."""
+    rng = np.random.default_rng(4)
+    lens = [int(x) for x in rng.integers(128, 16385, size=16)]
+    err, _ = _decoder_case(len(lens), lens, False, threads=16)
+    assert err < TOL, err

@@ -1,0 +1,102 @@
+"""The persistent planner (decode.cu:65-108), through the C ABI and the oracle.
+
+Pinned by the reference's own data: the (ctas, segments) columns of the 68
+rows of results/h100_{sweep,pagesize,ctas}.csv (tests/golden/planner_rows.csv),
+replayed at the reference's tile (64 tokens) and requested grid. Then the
+product planner must equal the oracle's independent restatement exactly, and
+satisfy the schedule's invariants, on random ragged batches.
+"""
+
+import csv
+import pathlib
+
+import numpy as np
+import pytest
+
+import oracle
+import pa_amd
+
+GOLDEN = pathlib.Path(__file__).resolve().parent / "golden"
+
+
+def _rows():
+    with open(GOLDEN / "planner_rows.csv") as f:
+        return list(csv.DictReader(f))
+
+
+@pytest.mark.parametrize("row", _rows(), ids=lambda r: f"{r['source']}-{r['dtype']}-{r['batch']}x{r['seq_len']}-{r['requested']}")
+def test_reference_plan_shapes(row):
+    lens = [int(row["seq_len"])] * int(row["batch"])
+    plan = pa_amd.make_plan_tiled(int(row["tile"]), lens, int(row["hkv"]), int(row["requested"]))
+    assert plan.num_ctas == int(row["ctas"])
+    assert len(plan.segments) == int(row["segments"])
+    n, segs, _, _ = oracle.make_plan(int(row["tile"]), lens, int(row["hkv"]), int(row["requested"]))
+    assert n == int(row["ctas"]) and len(segs) == int(row["segments"])
+
+
+def _check_invariants(plan, lens, hkv, tile, requested):
+    segs = plan.segments
+    total = sum((L + tile - 1) // tile for L in lens) * hkv
+    per = -(-total // requested)
+    assert plan.num_ctas == -(-total // per)
+    cta = plan.cta_seg_begin
+    assert cta[0] == 0 and cta[-1] == len(segs) and np.all(np.diff(cta) >= 0)
+    # each unit covers at most `per` tiles
+    for u in range(plan.num_ctas):
+        s = segs[cta[u]:cta[u + 1]]
+        tiles = sum(-(-(int(t1) - int(t0)) // tile) for _, _, t0, t1 in s)
+        assert 0 < tiles <= per
+    # segments partition every item in token order
+    item = plan.item_seg_begin
+    assert item[0] == 0 and item[-1] == len(segs)
+    for b, L in enumerate(lens):
+        for h in range(hkv):
+            i = b * hkv + h
+            s = segs[item[i]:item[i + 1]]
+            assert len(s) >= 1
+            assert np.all(s[:, 0] == b) and np.all(s[:, 1] == h)
+            assert s[0, 2] == 0 and s[-1, 3] == L
+            assert np.all(s[1:, 2] == s[:-1, 3])
+            assert np.all(s[:, 2] % tile == 0) and np.all(s[:, 3] > s[:, 2])
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_product_equals_oracle_and_invariants(seed):
+    rng = np.random.default_rng(seed)
+    batch = int(rng.integers(1, 40))
+    lens = [int(x) for x in rng.integers(1, 20000, size=batch)]
+    hkv = int(rng.choice([1, 2, 4, 8]))
+    tile = int(rng.choice([16, 64]))
+    requested = int(rng.integers(1, 2048))
+    plan = pa_amd.make_plan_tiled(tile, lens, hkv, requested)
+    n, segs, cta, item = oracle.make_plan(tile, lens, hkv, requested)
+    assert plan.num_ctas == n
+    assert np.array_equal(plan.segments, segs)
+    assert np.array_equal(plan.cta_seg_begin, cta)
+    assert np.array_equal(plan.item_seg_begin, item)
+    _check_invariants(plan, lens, hkv, tile, requested)
+
+
+def test_make_plan_uses_kernel_tile_and_validates():
+    plan = pa_amd.make_plan(pa_amd.FP16, [8192] * 32, 32, 8, 128, 1024)
+    assert plan.tile == pa_amd.tile_tokens(pa_amd.FP16, 128, 4) == 16
+    _check_invariants(plan, [8192] * 32, 8, plan.tile, 1024)
+    assert plan.needs_merge
+    with pytest.raises(pa_amd.InvalidArgument, match="at least one token"):
+        pa_amd.make_plan(pa_amd.FP16, [5, 0], 32, 8, 128, 64)
+    with pytest.raises(pa_amd.InvalidArgument, match="multiple"):
+        pa_amd.make_plan(pa_amd.FP16, [5], 30, 8, 128, 64)
+    with pytest.raises(pa_amd.InvalidArgument, match="head_dim"):
+        pa_amd.make_plan(pa_amd.FP16, [5], 32, 8, 64, 64)
+    with pytest.raises(pa_amd.InvalidArgument, match="group"):
+        pa_amd.make_plan(pa_amd.FP8_E4M3, [5], 48, 3, 128, 64)
+
+
+def test_single_segment_rows_need_no_merge():
+    plan = pa_amd.make_plan_tiled(64, [100, 64, 1], 2, 6)
+    assert len(plan.segments) == 6 and not plan.needs_merge
+
+
+def test_empty_batch_gives_empty_plan():
+    plan = pa_amd.make_plan_tiled(64, [], 8, 100)
+    assert plan.num_ctas == 0 and len(plan.segments) == 0
