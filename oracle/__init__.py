@@ -75,6 +75,8 @@ def lib() -> ctypes.CDLL:
         L.orc_gather_dequant.argtypes = [_I, _P, _P, _I, _I, _I, _I, _I, _F, _P]
         L.orc_cpu_attention.argtypes = [_P, _P, _P, _P, _I, _I]
         L.orc_paged_decode.argtypes = [_I, _P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _F, _F, _P, _I]
+        L.orc_attention_pairs.restype = ctypes.c_double
+        L.orc_attention_pairs.argtypes = [_P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _I]
         L.orc_make_plan.restype = _I
         L.orc_make_plan.argtypes = [_I, _P, _I, _I, _I, _P, _I, _P, _I, _P, ctypes.POINTER(_I)]
         _lib = L
@@ -190,6 +192,35 @@ def paged_decode(dtype: int, q_bits: np.ndarray, k_cache: np.ndarray, v_cache: n
                            lens.ctypes.data, batch, num_q_heads, num_kv_heads, head_dim, page_size,
                            k_scale, v_scale, out.ctypes.data, threads)
     return out
+
+
+def attention_pairs(q: np.ndarray, K: list, V: list, seq_lens, num_kv_heads: int,
+                    threads: int = 1, use_reference: bool = False) -> tuple[np.ndarray, float]:
+    """Runs cpu_attention for every (row, query head) pair over gathered fp32
+    K/V (one [len][d] array per (row, kv head) item) on `threads` threads.
+
+    use_reference=True calls the reference's own compiled cpu_attention
+    (oracle/_ref); otherwise the restatement. Returns (out [B][Hq][d], seconds
+    of the threaded loop)."""
+    q = _c(q, np.float32)
+    B, hq, d = q.shape
+    lens = _c(np.asarray(seq_lens), np.int32)
+    items = B * num_kv_heads
+    assert len(K) == items and len(V) == items
+    Ks = [_c(k, np.float32) for k in K]
+    Vs = [_c(v, np.float32) for v in V]
+    kp = (ctypes.c_void_p * items)(*[k.ctypes.data for k in Ks])
+    vp = (ctypes.c_void_p * items)(*[v.ctypes.data for v in Vs])
+    fn = None
+    if use_reference:
+        R = ref_lib()
+        if R is None:
+            raise RuntimeError("oracle/_ref was not built")
+        fn = ctypes.cast(R._Z13cpu_attentionPKfS0_S0_Pfii, ctypes.c_void_p).value
+    out = np.zeros((B, hq, d), dtype=np.float32)
+    secs = lib().orc_attention_pairs(fn, q.ctypes.data, ctypes.addressof(kp), ctypes.addressof(vp),
+                                     lens.ctypes.data, B, hq, num_kv_heads, d, out.ctypes.data, threads)
+    return out, float(secs)
 
 
 def make_plan(tile: int, seq_lens, num_kv_heads: int, requested: int):

@@ -8,12 +8,14 @@
  * reference's CPU path. See pa_oracle.h for the reference lines each function
  * restates.
  */
+#define _POSIX_C_SOURCE 200809L
 #include "pa_oracle.h"
 
 #include <math.h>
 #include <pthread.h>
 #include <stdlib.h>
 #include <string.h>
+#include <time.h>
 
 /* ---- binary16 ----------------------------------------------------------- */
 
@@ -246,6 +248,51 @@ void orc_paged_decode(int dtype, const uint16_t* q, const void* k_cache, const v
     for (int t = 0; t < threads; t++) pthread_join(tid[t], NULL);
     free(tid);
     pthread_mutex_destroy(&job.lock);
+}
+
+typedef struct {
+    orc_attention_fn fn;
+    const float* q;
+    const float* const* K;
+    const float* const* V;
+    const int32_t* lens;
+    int batch, hq, hkv, hd;
+    float* out;
+    int next;
+    pthread_mutex_t lock;
+} pairs_job;
+
+static void* pairs_worker(void* arg) {
+    pairs_job* j = (pairs_job*)arg;
+    const int group = j->hq / j->hkv;
+    for (;;) {
+        pthread_mutex_lock(&j->lock);
+        const int pair = j->next++;
+        pthread_mutex_unlock(&j->lock);
+        if (pair >= j->batch * j->hq) break;
+        const int b = pair / j->hq, hq = pair % j->hq;
+        const int item = b * j->hkv + hq / group;
+        const size_t off = (size_t)pair * j->hd;
+        j->fn(j->q + off, j->K[item], j->V[item], j->out + off, j->lens[b], j->hd);
+    }
+    return NULL;
+}
+
+double orc_attention_pairs(orc_attention_fn fn, const float* q, const float* const* K,
+                           const float* const* V, const int32_t* lens, int batch, int num_q_heads,
+                           int num_kv_heads, int head_dim, float* out, int threads) {
+    pairs_job job = {fn ? fn : orc_cpu_attention, q, K, V, lens, batch, num_q_heads, num_kv_heads,
+                     head_dim, out, 0, PTHREAD_MUTEX_INITIALIZER};
+    if (threads < 1) threads = 1;
+    pthread_t* tid = (pthread_t*)malloc(sizeof(pthread_t) * (size_t)threads);
+    struct timespec t0, t1;
+    clock_gettime(CLOCK_MONOTONIC, &t0);
+    for (int t = 0; t < threads; t++) pthread_create(&tid[t], NULL, pairs_worker, &job);
+    for (int t = 0; t < threads; t++) pthread_join(tid[t], NULL);
+    clock_gettime(CLOCK_MONOTONIC, &t1);
+    free(tid);
+    pthread_mutex_destroy(&job.lock);
+    return (double)(t1.tv_sec - t0.tv_sec) + 1e-9 * (double)(t1.tv_nsec - t0.tv_nsec);
 }
 
 /* ---- planner ------------------------------------------------------------ */

@@ -64,6 +64,19 @@ void orc_paged_decode(int dtype, const uint16_t* q, const void* k_cache, const v
                       int head_dim, int page_size, float k_scale, float v_scale, float* out,
                       int threads);
 
+/* Signature of src/attention/cpu/attention.hpp cpu_attention(q, K, V, out, T, d). */
+typedef void (*orc_attention_fn)(const float* q, const float* K, const float* V, float* out, int T, int d);
+
+/* The CPU baseline's timed loop: for every (batch row b, query head hq) pair,
+ * fn(q[b][hq], K[item], V[item], out[b][hq], lens[b], head_dim) with
+ * item = b * num_kv_heads + hq / G, over already gathered and dequantized fp32
+ * K/V ([len][head_dim] per item). fn NULL = orc_cpu_attention. Pairs are taken
+ * from a shared counter by `threads` POSIX threads. Returns the wall seconds of
+ * the loop (thread start to join, CLOCK_MONOTONIC). */
+double orc_attention_pairs(orc_attention_fn fn, const float* q, const float* const* K,
+                           const float* const* V, const int32_t* lens, int batch, int num_q_heads,
+                           int num_kv_heads, int head_dim, float* out, int threads);
+
 /* decode.cu:65-108 make_plan, restated as interval intersection: unit u owns
  * global tiles [u*per, (u+1)*per), item i owns its tiles in (row, head) order;
  * every non-empty intersection is a segment (row, head, t0, min(t1, len)).
