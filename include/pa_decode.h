@@ -75,6 +75,8 @@ typedef struct pa_decode_params {
     int32_t         needs_merge;
     float*          partial_out;       /* [num_segments][group][head_dim] */
     float*          partial_lse;       /* [num_segments][group] */
+    int32_t         max_item_segments; /* most segments of one (row, kv head); sizes the
+                                          merge launch (0 = unknown). Set by bind. */
 } pa_decode_params;
 
 /* Thread-local message describing the last failed call ("" if none). */
@@ -157,6 +159,11 @@ pa_status pa_gather_kv(int dtype, const void* cache, const int32_t* block_table_
  * (multiple of 16) with `blocks` x 256 threads; the cache flush and the
  * plain-copy ceiling. */
 pa_status pa_stream_read(const void* buf, size_t bytes, int blocks, uint32_t* sink, void* stream);
+/* The same read with threads_per_block in {256, 512}, unroll in {1, 2, 4, 8}
+ * independent 16 B loads per lane per trip, and optionally non-temporal loads:
+ * the copy-ceiling variants (bench_decode.cu:224-240 uses 512 threads, unroll 1). */
+pa_status pa_stream_read_ex(const void* buf, size_t bytes, int blocks, int threads_per_block, int unroll,
+                            int nontemporal, uint32_t* sink, void* stream);
 
 /* ---- host page pool (paged_kv_cache.cu:84-151, no device memory) -------- */
 

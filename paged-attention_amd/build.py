@@ -40,7 +40,7 @@ COMMON = [
     f"-I{CSRC}",
 ]
 
-SOURCES = ["pa_kernels.hip", "pa_capi.cpp"]
+SOURCES = ["pa_decode.hip", "pa_cache.hip", "pa_capi.cpp"]
 
 
 def _run(cmd: list[str]) -> None:
@@ -50,28 +50,34 @@ def _run(cmd: list[str]) -> None:
         raise RuntimeError(f"command failed ({proc.returncode}): {' '.join(cmd)}")
 
 
-def build(verbose: bool = False) -> pathlib.Path:
-    OBJ_DIR.mkdir(exist_ok=True)
-    LIB_DIR.mkdir(exist_ok=True)
+def build(verbose: bool = False, defines: list[str] | None = None, lib: pathlib.Path | None = None,
+          obj_dir: pathlib.Path | None = None) -> pathlib.Path:
+    """Compiles SOURCES and links `lib` (default lib/libpa_decode.so). `defines`
+    are extra -D options (the kernels' compile-time tuning knobs)."""
+    lib = lib or LIB
+    obj_dir = obj_dir or OBJ_DIR
+    obj_dir.mkdir(parents=True, exist_ok=True)
+    lib.parent.mkdir(parents=True, exist_ok=True)
+    extra = [f"-D{d}" for d in (defines or [])]
     jobs = []
     objs = []
     for src in SOURCES:
-        obj = OBJ_DIR / (src + ".o")
+        obj = obj_dir / (src + ".o")
         lang = ["-x", "hip"] if src.endswith(".hip") else []
-        jobs.append([HIPCC, *COMMON, *lang, "-c", str(CSRC / src), "-o", str(obj)])
+        jobs.append([HIPCC, *COMMON, *extra, *lang, "-c", str(CSRC / src), "-o", str(obj)])
         objs.append(obj)
-    with ThreadPoolExecutor(max_workers=len(jobs)) as ex:
+    if verbose:
         for cmd in jobs:
-            if verbose:
-                print(" ".join(cmd), flush=True)
+            print(" ".join(cmd), flush=True)
+    with ThreadPoolExecutor(max_workers=len(jobs)) as ex:
         list(ex.map(_run, jobs))
-    tmp = LIB.with_suffix(".so.tmp")
+    tmp = lib.with_suffix(".so.tmp")
     link = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
     if verbose:
         print(" ".join(link), flush=True)
     _run(link)
-    os.replace(tmp, LIB)
-    return LIB
+    os.replace(tmp, lib)
+    return lib
 
 
 if __name__ == "__main__":

@@ -1,0 +1,174 @@
+// gfx950 kernels around the decode path:
+//
+//   append_kernel        fp16 copy / FP8 E4M3 quantize + page scatter (paged_kv_cache.cu:15-39)
+//   gather_kernel        block-table resolution probe (the decode kernel's row address function)
+//   stream_read_kernel   streaming read: cache flush and plain-copy ceiling (bench_decode.cu:70-78)
+
+#include "pa_device.hpp"
+
+#include <cmath>
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+#include <type_traits>
+
+namespace pa {
+namespace {
+
+// ---------------------------------------------------------------------------
+// FP8 E4M3 encoder, written from the OCP OFP8 definition (bias 7, max normal
+// 448 = S.1111.110, NaN = S.1111.111, subnormals m * 2^-9): round to nearest
+// even, finite overflow and infinities saturate to +-448, NaN stays NaN.
+__device__ __forceinline__ uint32_t e4m3_encode(float x) {
+    const uint32_t u    = __builtin_bit_cast(uint32_t, x);
+    const uint32_t sign = (u >> 24) & 0x80u;
+    const uint32_t a    = u & 0x7fffffffu;
+    if (a > 0x7f800000u) return sign | 0x7fu;    // NaN
+    if (a >= 0x43e00000u) return sign | 0x7eu;   // |x| >= 448: saturate
+    if (a < 0x3c800000u) {                       // |x| < 2^-6: subnormal grid
+        const float ax = __builtin_bit_cast(float, a);
+        return sign | static_cast<uint32_t>(rintf(ax * 512.0f));   // 0..8; 8 is the min normal
+    }
+    const uint32_t man = a & 0x7fffffu;
+    uint32_t q = (((a >> 23) - 120u) << 3) | (man >> 20);
+    const uint32_t rem = man & 0xfffffu;
+    if (rem > 0x80000u || (rem == 0x80000u && (q & 1u))) q += 1u;
+    return sign | q;
+}
+
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t h16) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(h16)));
+}
+
+// One thread per (token, kv head, 8-dim chunk).
+template <int EB>
+__global__ __launch_bounds__(256) void append_kernel(const uint16_t* __restrict__ k,
+                                                     const uint16_t* __restrict__ v, void* k_cache,
+                                                     void* v_cache, const int32_t* __restrict__ bt_row,
+                                                     int start_pos, int n, int hkv, int page_size,
+                                                     float inv_k, float inv_v) {
+    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= n * hkv * (kHeadDim / 8)) return;
+    const int chunk = idx & 15;
+    const int th    = idx >> 4;
+    const int h     = th % hkv;
+    const int i     = th / hkv;
+    const int pos   = start_pos + i;
+    const int page  = bt_row[pos / page_size];
+    const size_t dst = kv_row_offset<EB>(page, h, pos % page_size, page_size, hkv) + 8 * EB * chunk;
+    const size_t src = (static_cast<size_t>(i) * hkv + h) * kHeadDim + 8 * chunk;
+    const u32x4 kin  = *reinterpret_cast<const u32x4*>(k + src);
+    const u32x4 vin  = *reinterpret_cast<const u32x4*>(v + src);
+    unsigned char* kc = static_cast<unsigned char*>(k_cache) + dst;
+    unsigned char* vc = static_cast<unsigned char*>(v_cache) + dst;
+    if constexpr (EB == 2) {
+        *reinterpret_cast<u32x4*>(kc) = kin;
+        *reinterpret_cast<u32x4*>(vc) = vin;
+    } else {
+        u32x2 ko = {0u, 0u}, vo = {0u, 0u};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const uint32_t kh = (kin[e >> 1] >> (16 * (e & 1))) & 0xffffu;
+            const uint32_t vh = (vin[e >> 1] >> (16 * (e & 1))) & 0xffffu;
+            ko[e >> 2] |= e4m3_encode(f16_bits_to_f32(kh) * inv_k) << (8 * (e & 3));
+            vo[e >> 2] |= e4m3_encode(f16_bits_to_f32(vh) * inv_v) << (8 * (e & 3));
+        }
+        *reinterpret_cast<u32x2*>(kc) = ko;
+        *reinterpret_cast<u32x2*>(vc) = vo;
+    }
+}
+
+// One thread per (token, 8-dim chunk) of one kv head: raw cache bytes out,
+// addressed with kv_row_offset, the row function the decode kernel uses.
+template <int EB>
+__global__ __launch_bounds__(256) void gather_kernel(const void* cache, const int32_t* __restrict__ bt_row,
+                                                     int hkv, int page_size, int kv_head, int len, void* out) {
+    using Raw = std::conditional_t<EB == 2, u32x4, u32x2>;
+    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= len * 16) return;
+    const int chunk = idx & 15;
+    const int t     = idx >> 4;
+    const int page  = bt_row[t / page_size];
+    const size_t off = kv_row_offset<EB>(page, kv_head, t % page_size, page_size, hkv) + 8 * EB * chunk;
+    *reinterpret_cast<Raw*>(static_cast<unsigned char*>(out) + static_cast<size_t>(t) * kRowBytes<EB> +
+                            8 * EB * chunk) =
+        *reinterpret_cast<const Raw*>(static_cast<const unsigned char*>(cache) + off);
+}
+
+// Streaming read of n 16-byte words, U independent loads per lane per trip
+// (U = 1 is bench_decode.cu:70-78's read_kernel); NT marks the loads
+// non-temporal so they bypass cache allocation.
+template <int U, bool NT>
+__global__ __launch_bounds__(512) void stream_read_kernel(const u32x4* __restrict__ x, size_t n,
+                                                          uint32_t* sink) {
+    uint32_t acc = 0;
+    const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+    size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    for (; i + (U - 1) * stride < n; i += U * stride) {
+        u32x4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) v[u] = NT ? __builtin_nontemporal_load(x + i + u * stride) : x[i + u * stride];
+#pragma unroll
+        for (int u = 0; u < U; ++u) acc ^= v[u][0] ^ v[u][1] ^ v[u][2] ^ v[u][3];
+    }
+    for (; i < n; i += stride) {
+        const u32x4 v = x[i];
+        acc ^= v[0] ^ v[1] ^ v[2] ^ v[3];
+    }
+    if (acc == 0x12345678u) *sink = acc;   // keeps the loads alive
+}
+
+}  // namespace
+
+hipError_t launch_append(int dtype, const uint16_t* k, const uint16_t* v, void* k_cache, void* v_cache,
+                         const int32_t* bt_row, int start_pos, int n, int hkv, int page_size, float inv_k,
+                         float inv_v, hipStream_t s) {
+    check_kv_dtype(dtype);
+    if (n <= 0) return hipSuccess;
+    const long threads = static_cast<long>(n) * hkv * (kHeadDim / 8);
+    const int blocks   = static_cast<int>((threads + 255) / 256);
+    if (dtype == PA_KV_FP16)
+        hipLaunchKernelGGL(append_kernel<2>, dim3(blocks), dim3(256), 0, s, k, v, k_cache, v_cache, bt_row,
+                           start_pos, n, hkv, page_size, inv_k, inv_v);
+    else
+        hipLaunchKernelGGL(append_kernel<1>, dim3(blocks), dim3(256), 0, s, k, v, k_cache, v_cache, bt_row,
+                           start_pos, n, hkv, page_size, inv_k, inv_v);
+    return hipGetLastError();
+}
+
+hipError_t launch_gather(int dtype, const void* cache, const int32_t* bt_row, int hkv, int page_size,
+                         int kv_head, int len, void* out, hipStream_t s) {
+    check_kv_dtype(dtype);
+    if (len <= 0) return hipSuccess;
+    const int blocks = (len * 16 + 255) / 256;
+    if (dtype == PA_KV_FP16)
+        hipLaunchKernelGGL(gather_kernel<2>, dim3(blocks), dim3(256), 0, s, cache, bt_row, hkv, page_size, kv_head,
+                           len, out);
+    else
+        hipLaunchKernelGGL(gather_kernel<1>, dim3(blocks), dim3(256), 0, s, cache, bt_row, hkv, page_size, kv_head,
+                           len, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_stream_read(const void* buf, size_t bytes, int blocks, int threads, int unroll, bool nt,
+                              uint32_t* sink, hipStream_t s) {
+    if (threads != 256 && threads != 512) throw std::invalid_argument("stream_read: threads must be 256 or 512");
+    const auto* x = static_cast<const u32x4*>(buf);
+    const size_t n = bytes / 16;
+#define PA_READ(U, NT) hipLaunchKernelGGL((stream_read_kernel<U, NT>), dim3(blocks), dim3(threads), 0, s, x, n, sink)
+    switch (unroll * 2 + (nt ? 1 : 0)) {
+        case 2: PA_READ(1, false); break;
+        case 3: PA_READ(1, true); break;
+        case 4: PA_READ(2, false); break;
+        case 5: PA_READ(2, true); break;
+        case 8: PA_READ(4, false); break;
+        case 9: PA_READ(4, true); break;
+        case 16: PA_READ(8, false); break;
+        case 17: PA_READ(8, true); break;
+        default: throw std::invalid_argument("stream_read: unroll must be 1, 2, 4 or 8");
+    }
+#undef PA_READ
+    return hipGetLastError();
+}
+
+}  // namespace pa

@@ -39,6 +39,7 @@ struct pa_device_plan {
     size_t   seg_cap = 0, cta_cap = 0, item_cap = 0, part_cap = 0;
     int      num_ctas    = 0;
     int      needs_merge = 0;
+    int      max_item_segments = 0;
 };
 
 // Host page allocator and per-slot block tables (paged_kv_cache.hpp:89-92).
@@ -218,6 +219,9 @@ void device_plan_upload(pa_device_plan& dp, const pa_plan& plan, int group, int 
     dp.partial_lse = dp.partial_out ? dp.partial_out + rows * head_dim : nullptr;
     dp.num_ctas    = plan.num_ctas;
     dp.needs_merge = nseg > static_cast<size_t>(plan.items) ? 1 : 0;
+    dp.max_item_segments = 0;
+    for (int i = 0; i < plan.items; ++i)
+        dp.max_item_segments = std::max(dp.max_item_segments, plan.item_seg_begin[i + 1] - plan.item_seg_begin[i]);
     // The sources are host vectors the caller may free or rebuild right away.
     pa::hip_check(hipStreamSynchronize(s), "hipStreamSynchronize");
 }
@@ -230,6 +234,7 @@ void device_plan_bind(const pa_device_plan& dp, pa_decode_params& p) {
     p.needs_merge    = dp.needs_merge;
     p.partial_out    = dp.partial_out;
     p.partial_lse    = dp.partial_lse;
+    p.max_item_segments = dp.max_item_segments;
 }
 
 void device_plan_free(pa_device_plan& dp) {
@@ -505,9 +510,16 @@ pa_status pa_gather_kv(int dtype, const void* cache, const int32_t* block_table_
 }
 
 pa_status pa_stream_read(const void* buf, size_t bytes, int blocks, uint32_t* sink, void* stream) {
+    return pa_stream_read_ex(buf, bytes, blocks, 256, 1, 0, sink, stream);
+}
+
+pa_status pa_stream_read_ex(const void* buf, size_t bytes, int blocks, int threads, int unroll, int nontemporal,
+                            uint32_t* sink, void* stream) {
     return guarded([&] {
         if (bytes % 16 != 0 || blocks <= 0 || !buf || !sink) throw std::invalid_argument("stream_read: bad arguments");
-        pa::hip_check(pa::launch_stream_read(buf, bytes, blocks, sink, as_stream(stream)), "read kernel launch");
+        pa::hip_check(pa::launch_stream_read(buf, bytes, blocks, threads, unroll, nontemporal != 0, sink,
+                                             as_stream(stream)),
+                      "read kernel launch");
     });
 }
 

@@ -1,0 +1,783 @@
+// gfx950 (MI355X) split-KV paged decode and its log-sum-exp merge.
+//
+//   decode_split_kernel_*  per-segment attention over HND pages (decode_kernels.cuh:123-403)
+//   decode_merge_kernel    LSE-weighted merge of split rows      (decode_kernels.cuh:409-432)
+//
+// Split kernel design (one wave64 = one work unit of the persistent plan):
+//   * A wave streams its own contiguous list of (row, kv head, token range)
+//     segments in steps of NG = 16 or 32 tokens (two 16-token halves), DEPTH
+//     steps of K/V in flight in registers. The pages of a step are looked up
+//     another DEPTH steps ahead, so an HBM load never waits on the block table.
+//   * K is fetched token-major: in each 16-token half, lane (c, kb) holds
+//     token c and a quarter of its dims. That is the A-operand layout of
+//     v_mfma_f32_16x16x32_f16 for S^T = K Q^T with the G query heads sharing
+//     the kv head as B columns, so K never goes through LDS.
+//   * V is fetched dim-major: lane (c, kb) holds tokens 4kb..4kb+3 of each
+//     half, dims 8c..8c+7. After a v_perm regroup that is the B operand of the
+//     P V MFMA (MFMA j <-> dims 8c + j): 16x16x16 for 16-token steps, 16x16x32
+//     with the two halves as one k-block for 32-token steps. The S^T
+//     accumulators are already the A-operand layout of P, so P never leaves
+//     registers.
+//   * When the page size is a power of two >= 16, a 16-token half lies in one
+//     page: one wave-uniform scalar lookup per half, and each load is a raw
+//     buffer load from an SGPR resource based at the half's first row, with
+//     constant lane offsets. The resource's range is the half's valid tokens,
+//     so loads past a segment's end (and every load of a slot past the unit's
+//     last step) return zeros without touching memory, and every slot issues
+//     the same loads, which keeps the hardware wait counts exact. Other page
+//     sizes resolve pages per lane with plain loads.
+//   * Online softmax in base 2 with a lazy running max: probabilities use a
+//     reference max per head that only moves (with the exact O/l rescale) when
+//     a score exceeds it by more than 2^8, so the cross-lane max reduction is
+//     paid at a segment's first step and then almost never. P <= 256 stays far
+//     inside fp16 range and l in fp32.
+//   * FP8 E4M3 is widened to fp16 in registers (exact); k_scale folds into the
+//     softmax scale and v_scale into the output normalization.
+//   * Q of each segment is fetched compactly (G x 256 B across the wave) with
+//     the segment's first K/V loads and expanded to the B-operand layout
+//     through a per-wave LDS slot once per segment.
+
+#include "pa_device.hpp"
+
+#include <cmath>
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+#include <type_traits>
+
+// Compile-time tuning knobs, per cache element type.
+// Tokens per step of the power-of-two page path (16 or 32).
+#ifndef PA_FP16_STEP
+#define PA_FP16_STEP 16
+#endif
+#ifndef PA_FP8_STEP
+#define PA_FP8_STEP 32
+#endif
+// Steps of K/V in flight per wave.
+#ifndef PA_FP16_DEPTH
+#define PA_FP16_DEPTH 4
+#endif
+#ifndef PA_FP8_DEPTH
+#define PA_FP8_DEPTH 3
+#endif
+// 1: K/V loads are non-temporal (streamed once, kept out of the caches).
+#ifndef PA_FP16_NONTEMPORAL
+#define PA_FP16_NONTEMPORAL 1
+#endif
+#ifndef PA_FP8_NONTEMPORAL
+#define PA_FP8_NONTEMPORAL 1
+#endif
+// Waves per SIMD the split kernel is register-budgeted for.
+#ifndef PA_FP16_WAVES_PER_EU
+#define PA_FP16_WAVES_PER_EU 2
+#endif
+#ifndef PA_FP8_WAVES_PER_EU
+#define PA_FP8_WAVES_PER_EU 2
+#endif
+// K lane layout. 1: lane (c, kb) load j holds token c, dims 32j + 8kb .. +7
+// (MFMA j's A operand in natural dim order; one load instruction covers 16
+// rows x 64 B (fp16) / 32 B (fp8) contiguous). 0: lane (c, kb) holds dims
+// 32kb .. 32kb+31 in 16-byte loads (half the fp8 load instructions; each
+// instruction touches 4 x 16 B spread over every row).
+#ifndef PA_FP16_K_NATURAL
+#define PA_FP16_K_NATURAL 1
+#endif
+#ifndef PA_FP8_K_NATURAL
+#define PA_FP8_K_NATURAL 0
+#endif
+
+namespace pa {
+namespace {
+
+constexpr int   kWaves        = 4;      // waves (work units) per 256-thread block
+constexpr float kRescaleSlack = 8.0f;   // log2 headroom of the lazy running max
+constexpr float kLog2e        = 1.4426950408889634f;
+// dword 3 of a raw buffer resource (32-bit data format, no swizzle), and the
+// cache-policy operand of buffer loads (2 = non-temporal).
+constexpr int kBufferFlags = 0x00020000;
+template <bool NT> constexpr int kAux = NT ? 2 : 0;
+
+template <int EB> struct Tune {
+    static constexpr int  step  = EB == 2 ? PA_FP16_STEP : PA_FP8_STEP;
+    static constexpr int  depth = EB == 2 ? PA_FP16_DEPTH : PA_FP8_DEPTH;
+    static constexpr bool nt    = EB == 2 ? PA_FP16_NONTEMPORAL != 0 : PA_FP8_NONTEMPORAL != 0;
+    static constexpr bool knat  = EB == 2 ? PA_FP16_K_NATURAL != 0 : PA_FP8_K_NATURAL != 0;
+};
+static_assert(Tune<2>::step == 16 || Tune<2>::step == 32, "fp16 step must be 16 or 32");
+static_assert(Tune<1>::step == 16 || Tune<1>::step == 32, "fp8 step must be 16 or 32");
+
+// How a step finds its pages.
+enum PagePath : int {
+    kPagePow2 = 0,   // page_size a power of two >= 16: a 16-token half is in one page
+    kPageQuad = 1,   // page_size 4 or 8: one lookup per lane for K and one for V
+    kPageAny  = 2,   // any other page size: one lookup per token, integer division
+};
+
+// One position of a wave's schedule: the current step of the current segment.
+// Every field is wave-uniform.
+struct Cursor {
+    int seg;
+    int b, h;    // batch row, kv head
+    int tok;     // first token of the step
+    int t0, w;   // segment start and end (exclusive)
+};
+
+__device__ __forceinline__ void cursor_load(Cursor& c, const int4* segs) {
+    const int4 s = segs[c.seg];
+    c.b   = s.x;
+    c.h   = s.y;
+    c.tok = s.z;
+    c.t0  = s.z;
+    c.w   = s.w;
+}
+
+// Moves to the next step: 0 = same segment, 1 = next segment, -1 = none (the
+// cursor stays on its last step).
+template <int NG>
+__device__ __forceinline__ int cursor_step(Cursor& c, const int4* segs, int seg_end) {
+    if (__builtin_expect(c.tok + NG < c.w, 1)) {
+        c.tok += NG;
+        return 0;
+    }
+    if (c.seg + 1 >= seg_end) return -1;
+    c.seg++;
+    cursor_load(c, segs);
+    return 1;
+}
+
+// Block-table row of batch row b (decode_kernels.cuh:150-153).
+__device__ __forceinline__ const int* table_row(const pa_decode_params& p, int b) {
+    const int slot = p.slot_ids ? p.slot_ids[b] : b;
+    return p.block_table + static_cast<size_t>(slot) * p.block_table_stride;
+}
+
+// arr[4 * kb + i] for the heads a lane's O rows hold (kb only matters for G = 8).
+template <int G>
+__device__ __forceinline__ float head_pick(const float (&arr)[G], int kb, int i) {
+    if constexpr (G > 4) return kb ? arr[4 + i] : arr[i];
+    else return arr[i < G ? i : 0];
+}
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, int bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, kBufferFlags);
+}
+
+// ---------------------------------------------------------------------------
+// Split kernel body.
+//   EB    cache element bytes (2 fp16, 1 fp8)
+//   G     query heads per kv head (1, 2, 4, 8)
+//   NG    tokens per step (16 or 32)
+//   DEPTH steps of K/V in flight per wave
+//   PATH  page resolution (PagePath)
+template <int EB, int G, int NG, int DEPTH, int PATH>
+__device__ __forceinline__ void decode_split_body(const pa_decode_params& p, int page_shift) {
+    constexpr int  NH    = NG / 16;                 // 16-token halves per step
+    constexpr int  ROW   = kRowBytes<EB>;           // bytes per token row
+    constexpr bool NT    = Tune<EB>::nt;
+    constexpr bool KNAT  = Tune<EB>::knat;
+    constexpr int  KL    = KNAT ? 8 * EB : 16;      // bytes per K load
+    constexpr int  NK    = KNAT ? 4 : ROW / 64;     // K loads per lane per half
+    constexpr int  KSTEP = KNAT ? 32 * EB : 16;     // byte distance between a lane's K loads
+    constexpr int  KLANE = KNAT ? KL : ROW / 4;     // byte offset of k-block kb in a row
+    constexpr int  VCH   = 8 * EB;                  // V bytes per lane per token (8 dims)
+    constexpr int  NQ    = G > 4 ? 2 : 1;           // compact Q registers per lane
+    constexpr int  NVL   = PATH == kPageAny ? 4 : 1;   // V page lookups per lane (per-lane paths)
+    constexpr int  HW    = G < 4 ? G : 4;           // live O rows per writing lane
+    using VRaw = std::conditional_t<EB == 2, u32x4, u32x2>;
+    using KRaw = std::conditional_t<KL == 16, u32x4, u32x2>;
+
+    __shared__ __attribute__((aligned(16))) u32x4 q_lds[kWaves][16 * G];   // G heads x 256 B per wave
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int unit = blockIdx.x * kWaves + wave;
+    if (unit >= p.num_ctas) return;
+    const int seg_begin = p.cta_seg_begin[unit];
+    const int seg_end   = p.cta_seg_begin[unit + 1];
+    if (seg_begin >= seg_end) return;
+
+    const int c  = lane & 15;   // MFMA column / row index within a 16-block
+    const int kb = lane >> 4;   // MFMA k-block
+    const int4* segs = reinterpret_cast<const int4*>(p.segments);
+    const unsigned char* kbase = static_cast<const unsigned char*>(p.k_cache);
+    const unsigned char* vbase = static_cast<const unsigned char*>(p.v_cache);
+    const int P   = p.page_size;
+    const int hkv = p.num_kv_heads;
+    const int hq  = p.num_q_heads;
+    const float qk_scale = p.sm_scale * p.k_scale * kLog2e;   // softmax in base 2
+    const uint32_t page_bytes = static_cast<uint32_t>(hkv * P * ROW);   // one page of one pool
+    // Constant lane offsets inside a 16-token half (power-of-two path).
+    const int k_lane_off = c * ROW + kb * KLANE;
+    const int v_lane_off = 4 * kb * ROW + c * VCH;
+
+    // ---- pipeline registers, indexed by ring slot = step index mod DEPTH
+    KRaw  kr[DEPTH][NH][NK];   // K: token 16hh + c of each half
+    VRaw  vr[DEPTH][NH][4];    // V: tokens 16hh + 4kb + r, dims 8c..8c+7
+    u32x4 qc[DEPTH][NQ];       // compact Q, loaded with a segment's first step
+    int   pg[DEPTH][NH];       // power-of-two path: page of each half (wave-uniform)
+    int   pk[DEPTH][NH], sk[DEPTH][NH];            // per-lane paths: K token's page and slot
+    int   pv[DEPTH][NH][NVL], sv[DEPTH][NH][NVL];  // per-lane paths: V tokens' page(s) and slot(s)
+
+    Cursor C, L, T;
+    C.seg = seg_begin;
+    cursor_load(C, segs);
+    L = C;
+    T = C;
+    const int* t_row = table_row(p, T.b);
+    bool t_more = true, l_more = true;
+
+    // Page lookups of step T into slot s, then advance T.
+    auto lookup = [&](int s) {
+        if constexpr (PATH == kPagePow2) {
+            if (t_more) {
+#pragma unroll
+                for (int hh = 0; hh < NH; ++hh) pg[s][hh] = t_row[min(T.tok + 16 * hh, T.w - 1) >> page_shift];
+            }
+        } else {
+            // Per-lane lookups repeat T's last step once it is exhausted, so
+            // that every slot issues the same vector loads.
+            const int last = T.w - 1;
+#pragma unroll
+            for (int hh = 0; hh < NH; ++hh) {
+                const int tk = min(T.tok + 16 * hh + c, last);
+                const int qk = PATH == kPageQuad ? (tk >> page_shift) : tk / P;
+                pk[s][hh] = t_row[qk];
+                sk[s][hh] = tk - qk * P;
+                if constexpr (PATH == kPageQuad) {
+                    // The lane's 4 V tokens share one page (page_size % 4 == 0).
+                    const int tv = min(T.tok + 16 * hh + 4 * kb, last & ~3);
+                    const int qv = tv >> page_shift;
+                    pv[s][hh][0] = t_row[qv];
+                    sv[s][hh][0] = tv - qv * P;
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int t  = min(T.tok + 16 * hh + 4 * kb + r, last);
+                        const int qv = t / P;
+                        pv[s][hh][r] = t_row[qv];
+                        sv[s][hh][r] = t - qv * P;
+                    }
+                }
+            }
+        }
+        if (t_more) {
+            const int a = cursor_step<NG>(T, segs, seg_end);
+            if (__builtin_expect(a != 0, 0)) {
+                if (a < 0) t_more = false;
+                else t_row = table_row(p, T.b);
+            }
+        }
+    };
+
+    // K/V loads of step L into slot s (and Q at a segment start), then advance L.
+    auto issue = [&](int s) {
+        const bool first = l_more && L.tok == L.t0;
+        const __amdgpu_buffer_rsrc_t qrs =
+            buffer_rsrc(p.q + (static_cast<size_t>(L.b) * hq + L.h * G) * kHeadDim, first ? 256 * G : 0);
+#pragma unroll
+        for (int n = 0; n < NQ; ++n)
+            qc[s][n] = __builtin_bit_cast(
+                u32x4, __builtin_amdgcn_raw_buffer_load_b128(qrs, 16 * ((64 * n + lane) % (16 * G)), 0, 0));
+        if constexpr (PATH == kPagePow2) {
+#pragma unroll
+            for (int hh = 0; hh < NH; ++hh) {
+                const int t  = L.tok + 16 * hh;          // first token of the half
+                const int bt = min(t, L.w - 1);          // a token of the sequence (pages stay in range)
+                const int nv = l_more ? max(0, min(16, L.w - t)) : 0;   // valid tokens of the half
+                const size_t row0 = static_cast<size_t>(pg[s][hh]) * page_bytes +
+                                    static_cast<uint32_t>((L.h * P + (bt & (P - 1))) * ROW);
+                const __amdgpu_buffer_rsrc_t krs = buffer_rsrc(kbase + row0, nv * ROW);
+                const __amdgpu_buffer_rsrc_t vrs = buffer_rsrc(vbase + row0, nv * ROW);
+#pragma unroll
+                for (int u = 0; u < NK; ++u) {
+                    if constexpr (KL == 16)
+                        kr[s][hh][u] = __builtin_bit_cast(
+                            u32x4, __builtin_amdgcn_raw_buffer_load_b128(krs, k_lane_off + KSTEP * u, 0, kAux<NT>));
+                    else
+                        kr[s][hh][u] = __builtin_bit_cast(
+                            u32x2, __builtin_amdgcn_raw_buffer_load_b64(krs, k_lane_off + KSTEP * u, 0, kAux<NT>));
+                }
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    if constexpr (EB == 2)
+                        vr[s][hh][r] = __builtin_bit_cast(
+                            u32x4, __builtin_amdgcn_raw_buffer_load_b128(vrs, v_lane_off + r * ROW, 0, kAux<NT>));
+                    else
+                        vr[s][hh][r] = __builtin_bit_cast(
+                            u32x2, __builtin_amdgcn_raw_buffer_load_b64(vrs, v_lane_off + r * ROW, 0, kAux<NT>));
+                }
+            }
+        } else {
+#pragma unroll
+            for (int hh = 0; hh < NH; ++hh) {
+                const unsigned char* kp = kbase + kv_row_offset<EB>(pk[s][hh], L.h, sk[s][hh], P, hkv) + kb * KLANE;
+#pragma unroll
+                for (int u = 0; u < NK; ++u) {
+                    if constexpr (KL == 16) kr[s][hh][u] = load16<NT>(kp + KSTEP * u);
+                    else kr[s][hh][u] = load8<NT>(kp + KSTEP * u);
+                }
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    size_t off;
+                    if constexpr (PATH == kPageQuad) {
+                        const int tv = min(L.tok + 16 * hh + 4 * kb, (L.w - 1) & ~3);
+                        off = kv_row_offset<EB>(pv[s][hh][0], L.h, sv[s][hh][0] + min(r, L.w - 1 - tv), P, hkv);
+                    } else {
+                        off = kv_row_offset<EB>(pv[s][hh][r], L.h, sv[s][hh][r], P, hkv);
+                    }
+                    if constexpr (EB == 2) vr[s][hh][r] = load16<NT>(vbase + off + c * VCH);
+                    else vr[s][hh][r] = load8<NT>(vbase + off + c * VCH);
+                }
+            }
+        }
+        if (l_more && cursor_step<NG>(L, segs, seg_end) < 0) l_more = false;
+    };
+
+    // ---- consumer state. m_run = -inf marks a segment start: the first step
+    // always takes the rescale path, which then sets the running max (the
+    // factor 2^-inf = 0 keeps O = 0 and l = 0).
+    u32x4 qf[4];      // B operand of QK MFMA j: Q[head c % G][the dims of K's A operand]
+    f32x4 oacc[8];    // O[head 4kb+i][dim 8c+j] = oacc[j][i]
+    float m_run = -INFINITY, l_run = 0.f;
+    bool  whole = false;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) oacc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    auto finish_segment = [&]() {
+        float lsum = l_run;
+        lsum += __shfl_xor(lsum, 16);
+        lsum += __shfl_xor(lsum, 32);
+        float m_h[G], inv_h[G];
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+            m_h[h]   = readlane_f(m_run, h);
+            inv_h[h] = readlane_f(lsum, h);
+        }
+        if (4 * kb < G) {   // lanes holding live O rows: heads 4kb .. 4kb + HW - 1
+            if (whole) {
+#pragma unroll
+                for (int i = 0; i < HW; ++i) {
+                    const float inv = p.v_scale / head_pick<G>(inv_h, kb, i);
+                    u32x4 o;
+#pragma unroll
+                    for (int jj = 0; jj < 4; ++jj) {
+                        const f16x2 h2 = {static_cast<_Float16>(oacc[2 * jj][i] * inv),
+                                          static_cast<_Float16>(oacc[2 * jj + 1][i] * inv)};
+                        o[jj] = __builtin_bit_cast(uint32_t, h2);
+                    }
+                    *reinterpret_cast<u32x4*>(p.out + (static_cast<size_t>(C.b) * hq + C.h * G + 4 * kb + i) *
+                                                          kHeadDim + 8 * c) = o;
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < HW; ++i) {
+                    const float lh  = head_pick<G>(inv_h, kb, i);
+                    const float inv = p.v_scale / lh;
+                    float* prow = p.partial_out + (static_cast<size_t>(C.seg) * G + 4 * kb + i) * kHeadDim + 8 * c;
+                    f32x4 lo, hi;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        lo[j] = oacc[j][i] * inv;
+                        hi[j] = oacc[4 + j][i] * inv;
+                    }
+                    *reinterpret_cast<f32x4*>(prow)     = lo;
+                    *reinterpret_cast<f32x4*>(prow + 4) = hi;
+                    if (c == 0)
+                        p.partial_lse[static_cast<size_t>(C.seg) * G + 4 * kb + i] =
+                            head_pick<G>(m_h, kb, i) + __log2f(lh);
+                }
+            }
+        }
+        m_run = -INFINITY;
+        l_run = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) oacc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    };
+
+    auto rescale = [&](float xmax) {
+        float mx = fmaxf(xmax, __shfl_xor(xmax, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float m_new = fmaxf(m_run, mx);
+        const float alpha = exp2_fast(m_run - m_new);
+        m_run = m_new;
+        l_run *= alpha;
+        float a_h[G];
+#pragma unroll
+        for (int h = 0; h < G; ++h) a_h[h] = readlane_f(alpha, h);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float ai = 4 * kb + i < G ? head_pick<G>(a_h, kb, i) : 1.0f;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) oacc[j][i] *= ai;
+        }
+    };
+
+    auto consume = [&](int s) {
+        if (__builtin_expect(C.tok == C.t0, 0)) {
+            // Q of the new segment: compact -> LDS -> B-operand layout.
+            u32x4* ql = q_lds[wave];
+#pragma unroll
+            for (int n = 0; n < NQ; ++n)
+                if (64 * n + lane < 16 * G) ql[64 * n + lane] = qc[s][n];
+            const int hc = c & (G - 1);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) qf[j] = ql[16 * hc + (KNAT ? 4 * j + kb : 4 * kb + j)];
+            const int item = C.b * hkv + C.h;
+            whole = p.item_seg_begin[item + 1] - p.item_seg_begin[item] == 1;
+        }
+        // S^T[token][head] per 16-token half; lane (c, kb) gets tokens 4kb+i.
+        float x[NH][4];
+#pragma unroll
+        for (int hh = 0; hh < NH; ++hh) {
+            f32x4 sacc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                f16x8 a;
+                if constexpr (EB == 2) {
+                    a = __builtin_bit_cast(f16x8, kr[s][hh][j]);
+                } else if constexpr (KNAT) {
+                    a = fp8x8_to_f16x8(kr[s][hh][j][0], kr[s][hh][j][1]);
+                } else {
+                    const KRaw w = kr[s][hh][j >> 1];
+                    a = fp8x8_to_f16x8(w[2 * (j & 1)], w[2 * (j & 1) + 1]);
+                }
+                sacc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, __builtin_bit_cast(f16x8, qf[j]), sacc, 0, 0, 0);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) x[hh][i] = sacc[i] * qk_scale;
+        }
+        const int lim = C.w - C.tok;   // valid tokens of the step
+        if (__builtin_expect(lim < NG, 0)) {
+#pragma unroll
+            for (int hh = 0; hh < NH; ++hh)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) x[hh][i] = 16 * hh + 4 * kb + i < lim ? x[hh][i] : -INFINITY;
+        }
+        float xmax = fmaxf(fmaxf(x[0][0], x[0][1]), fmaxf(x[0][2], x[0][3]));
+        if constexpr (NH > 1) xmax = fmaxf(xmax, fmaxf(fmaxf(x[1][0], x[1][1]), fmaxf(x[1][2], x[1][3])));
+        if (__builtin_expect(__builtin_amdgcn_ballot_w64(c < G && xmax > m_run + kRescaleSlack) != 0, 0))
+            rescale(xmax);
+        float pr[NH][4];
+        float psum = 0.f;
+#pragma unroll
+        for (int hh = 0; hh < NH; ++hh) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) pr[hh][i] = exp2_fast(x[hh][i] - m_run);
+            psum += (pr[hh][0] + pr[hh][1]) + (pr[hh][2] + pr[hh][3]);
+        }
+        l_run += psum;
+
+        // O[head][dim] += P[head][token] V[token][dim]; MFMA j covers dims 8c + j.
+        if constexpr (NH == 1) {
+            const f16x4 pa = {static_cast<_Float16>(pr[0][0]), static_cast<_Float16>(pr[0][1]),
+                              static_cast<_Float16>(pr[0][2]), static_cast<_Float16>(pr[0][3])};
+            if constexpr (EB == 2) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
+                    u32x2 bw;
+                    bw[0] = __builtin_amdgcn_perm(vr[s][0][1][j >> 1], vr[s][0][0][j >> 1], sel);
+                    bw[1] = __builtin_amdgcn_perm(vr[s][0][3][j >> 1], vr[s][0][2][j >> 1], sel);
+                    oacc[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, __builtin_bit_cast(f16x4, bw), oacc[j], 0, 0, 0);
+                }
+            } else {
+#pragma unroll
+                for (int w = 0; w < 2; ++w) {
+                    // bytes [t0 d, t1 d, t0 d+1, t1 d+1] for d = 4w (lo) and 4w+2 (hi)
+                    const uint32_t lo01 = __builtin_amdgcn_perm(vr[s][0][1][w], vr[s][0][0][w], 0x05010400u);
+                    const uint32_t hi01 = __builtin_amdgcn_perm(vr[s][0][1][w], vr[s][0][0][w], 0x07030602u);
+                    const uint32_t lo23 = __builtin_amdgcn_perm(vr[s][0][3][w], vr[s][0][2][w], 0x05010400u);
+                    const uint32_t hi23 = __builtin_amdgcn_perm(vr[s][0][3][w], vr[s][0][2][w], 0x07030602u);
+                    const u32x2 b0 = {fp8x2_to_f16x2<false>(lo01), fp8x2_to_f16x2<false>(lo23)};
+                    const u32x2 b1 = {fp8x2_to_f16x2<true>(lo01), fp8x2_to_f16x2<true>(lo23)};
+                    const u32x2 b2 = {fp8x2_to_f16x2<false>(hi01), fp8x2_to_f16x2<false>(hi23)};
+                    const u32x2 b3 = {fp8x2_to_f16x2<true>(hi01), fp8x2_to_f16x2<true>(hi23)};
+                    oacc[4 * w + 0] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, __builtin_bit_cast(f16x4, b0), oacc[4 * w + 0], 0, 0, 0);
+                    oacc[4 * w + 1] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, __builtin_bit_cast(f16x4, b1), oacc[4 * w + 1], 0, 0, 0);
+                    oacc[4 * w + 2] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, __builtin_bit_cast(f16x4, b2), oacc[4 * w + 2], 0, 0, 0);
+                    oacc[4 * w + 3] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, __builtin_bit_cast(f16x4, b3), oacc[4 * w + 3], 0, 0, 0);
+                }
+            }
+        } else {
+            // One 32-token k-block: k-index 8kb + i <-> token 4kb + i of half 0
+            // (i < 4) and token 16 + 4kb + (i - 4) of half 1.
+            const f16x8 pa = {static_cast<_Float16>(pr[0][0]), static_cast<_Float16>(pr[0][1]),
+                              static_cast<_Float16>(pr[0][2]), static_cast<_Float16>(pr[0][3]),
+                              static_cast<_Float16>(pr[1][0]), static_cast<_Float16>(pr[1][1]),
+                              static_cast<_Float16>(pr[1][2]), static_cast<_Float16>(pr[1][3])};
+            if constexpr (EB == 2) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
+                    const int d = j >> 1;
+                    u32x4 bw;
+                    bw[0] = __builtin_amdgcn_perm(vr[s][0][1][d], vr[s][0][0][d], sel);
+                    bw[1] = __builtin_amdgcn_perm(vr[s][0][3][d], vr[s][0][2][d], sel);
+                    bw[2] = __builtin_amdgcn_perm(vr[s][1][1][d], vr[s][1][0][d], sel);
+                    bw[3] = __builtin_amdgcn_perm(vr[s][1][3][d], vr[s][1][2][d], sel);
+                    oacc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, __builtin_bit_cast(f16x8, bw), oacc[j], 0, 0, 0);
+                }
+            } else {
+#pragma unroll
+                for (int w = 0; w < 2; ++w) {
+                    uint32_t lo01[2], hi01[2], lo23[2], hi23[2];
+#pragma unroll
+                    for (int hh = 0; hh < 2; ++hh) {
+                        lo01[hh] = __builtin_amdgcn_perm(vr[s][hh][1][w], vr[s][hh][0][w], 0x05010400u);
+                        hi01[hh] = __builtin_amdgcn_perm(vr[s][hh][1][w], vr[s][hh][0][w], 0x07030602u);
+                        lo23[hh] = __builtin_amdgcn_perm(vr[s][hh][3][w], vr[s][hh][2][w], 0x05010400u);
+                        hi23[hh] = __builtin_amdgcn_perm(vr[s][hh][3][w], vr[s][hh][2][w], 0x07030602u);
+                    }
+                    const u32x4 b0 = {fp8x2_to_f16x2<false>(lo01[0]), fp8x2_to_f16x2<false>(lo23[0]),
+                                      fp8x2_to_f16x2<false>(lo01[1]), fp8x2_to_f16x2<false>(lo23[1])};
+                    const u32x4 b1 = {fp8x2_to_f16x2<true>(lo01[0]), fp8x2_to_f16x2<true>(lo23[0]),
+                                      fp8x2_to_f16x2<true>(lo01[1]), fp8x2_to_f16x2<true>(lo23[1])};
+                    const u32x4 b2 = {fp8x2_to_f16x2<false>(hi01[0]), fp8x2_to_f16x2<false>(hi23[0]),
+                                      fp8x2_to_f16x2<false>(hi01[1]), fp8x2_to_f16x2<false>(hi23[1])};
+                    const u32x4 b3 = {fp8x2_to_f16x2<true>(hi01[0]), fp8x2_to_f16x2<true>(hi23[0]),
+                                      fp8x2_to_f16x2<true>(hi01[1]), fp8x2_to_f16x2<true>(hi23[1])};
+                    oacc[4 * w + 0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, __builtin_bit_cast(f16x8, b0), oacc[4 * w + 0], 0, 0, 0);
+                    oacc[4 * w + 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, __builtin_bit_cast(f16x8, b1), oacc[4 * w + 1], 0, 0, 0);
+                    oacc[4 * w + 2] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, __builtin_bit_cast(f16x8, b2), oacc[4 * w + 2], 0, 0, 0);
+                    oacc[4 * w + 3] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, __builtin_bit_cast(f16x8, b3), oacc[4 * w + 3], 0, 0, 0);
+                }
+            }
+        }
+        if (__builtin_expect(C.tok + NG >= C.w, 0)) finish_segment();
+    };
+
+    // ---- prologue: pages of steps 0..DEPTH-1, then their loads, each
+    // followed by the pages DEPTH steps further on.
+#pragma unroll
+    for (int s = 0; s < DEPTH; ++s) lookup(s);
+#pragma unroll
+    for (int s = 0; s < DEPTH; ++s) {
+        issue(s);
+        lookup(s);
+    }
+
+    // ---- steady state: consume step k, refill its slot with step k + DEPTH.
+    bool live = true;
+    while (live) {
+#pragma unroll
+        for (int s = 0; s < DEPTH; ++s) {
+            consume(s);
+            if (cursor_step<NG>(C, segs, seg_end) < 0) {
+                live = false;
+                break;
+            }
+            issue(s);
+            lookup(s);
+        }
+    }
+}
+
+// The kernels: one per element width, each with its own register budget.
+template <int G, int NG, int DEPTH, int PATH>
+__global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(PA_FP16_WAVES_PER_EU)))
+void decode_split_kernel_f16(const pa_decode_params p, int page_shift) {
+    decode_split_body<2, G, NG, DEPTH, PATH>(p, page_shift);
+}
+
+template <int G, int NG, int DEPTH, int PATH>
+__global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(PA_FP8_WAVES_PER_EU)))
+void decode_split_kernel_fp8(const pa_decode_params p, int page_shift) {
+    decode_split_body<1, G, NG, DEPTH, PATH>(p, page_shift);
+}
+
+// ---------------------------------------------------------------------------
+// Merge (decode_kernels.cuh:409-432): one block per (query head, batch row) of
+// a row split over n > 1 segments. Pass 1 takes the maximum base-2 LSE; pass 2
+// has each wave accumulate sum_s 2^(lse_s - max) o_s over every WAVES-th
+// segment (two dims per lane, loads unrolled), and the waves combine in LDS.
+template <int G, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void decode_merge_kernel(const pa_decode_params p) {
+    constexpr int NT = 64 * WAVES;
+    const int hqi  = blockIdx.x;
+    const int b    = blockIdx.y;
+    const int item = b * p.num_kv_heads + hqi / G;
+    const int g    = hqi % G;
+    const int s0   = p.item_seg_begin[item];
+    const int n    = p.item_seg_begin[item + 1] - s0;
+    if (n <= 1) return;
+
+    __shared__ float red[WAVES];
+    __shared__ float2 acc_lds[WAVES][64];
+    __shared__ float den_lds[WAVES];
+
+    const int t    = threadIdx.x;
+    const int lane = t & 63;
+    const int wave = t >> 6;
+    const float* lse = p.partial_lse + static_cast<size_t>(s0) * G + g;
+
+    float mx = -INFINITY;
+    for (int i = t; i < n; i += NT) mx = fmaxf(mx, lse[static_cast<size_t>(i) * G]);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    if (lane == 0) red[wave] = mx;
+    __syncthreads();
+    mx = red[0];
+#pragma unroll
+    for (int w = 1; w < WAVES; ++w) mx = fmaxf(mx, red[w]);
+
+    float n0 = 0.f, n1 = 0.f, den = 0.f;
+    const float* po = p.partial_out + (static_cast<size_t>(s0) * G + g) * kHeadDim + 2 * lane;
+#pragma unroll 8
+    for (int i = wave; i < n; i += WAVES) {
+        const float wgt = exp2_fast(lse[static_cast<size_t>(i) * G] - mx);
+        const float2 o  = *reinterpret_cast<const float2*>(po + static_cast<size_t>(i) * G * kHeadDim);
+        n0 = fmaf(wgt, o.x, n0);
+        n1 = fmaf(wgt, o.y, n1);
+        den += wgt;
+    }
+    acc_lds[wave][lane] = float2{n0, n1};
+    if (lane == 0) den_lds[wave] = den;
+    __syncthreads();
+    if (wave == 0) {
+        float a0 = 0.f, a1 = 0.f, d = 0.f;
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w) {
+            a0 += acc_lds[w][lane].x;
+            a1 += acc_lds[w][lane].y;
+            d += den_lds[w];
+        }
+        const f16x2 h2 = {static_cast<_Float16>(a0 / d), static_cast<_Float16>(a1 / d)};
+        *reinterpret_cast<uint32_t*>(p.out + (static_cast<size_t>(b) * p.num_q_heads + hqi) * kHeadDim + 2 * lane) =
+            __builtin_bit_cast(uint32_t, h2);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Dispatch.
+
+// Steps in flight on the per-lane page paths (they keep the power-of-two
+// path's step, so results do not depend on the page size).
+template <int EB> constexpr int kLaneDepth = Tune<EB>::step == 16 ? 3 : 2;
+
+template <int EB, int G, int NG, int DEPTH, int PATH>
+hipError_t launch_split_p(const pa_decode_params& p, int shift, hipStream_t s) {
+    const int blocks = (p.num_ctas + kWaves - 1) / kWaves;
+    if constexpr (EB == 2)
+        hipLaunchKernelGGL((decode_split_kernel_f16<G, NG, DEPTH, PATH>), dim3(blocks), dim3(64 * kWaves), 0, s, p,
+                           shift);
+    else
+        hipLaunchKernelGGL((decode_split_kernel_fp8<G, NG, DEPTH, PATH>), dim3(blocks), dim3(64 * kWaves), 0, s, p,
+                           shift);
+    return hipGetLastError();
+}
+
+template <int EB, int G>
+hipError_t launch_split_g(const pa_decode_params& p, hipStream_t s) {
+    const int  P     = p.page_size;
+    const bool pow2  = (P & (P - 1)) == 0;
+    const int  shift = pow2 ? __builtin_ctz(static_cast<unsigned>(P)) : 0;
+    if (pow2 && P >= 16) {
+        // Byte offsets of one page and of one (kv head, slot) inside it are 32-bit.
+        if (static_cast<long long>(p.num_kv_heads) * P * kRowBytes<EB> >= (1ll << 31))
+            throw std::invalid_argument("decode: page_size * num_kv_heads * row bytes must be below 2^31");
+        return launch_split_p<EB, G, Tune<EB>::step, Tune<EB>::depth, kPagePow2>(p, shift, s);
+    }
+    if (pow2 && P >= 4) return launch_split_p<EB, G, Tune<EB>::step, kLaneDepth<EB>, kPageQuad>(p, shift, s);
+    return launch_split_p<EB, G, Tune<EB>::step, kLaneDepth<EB>, kPageAny>(p, shift, s);
+}
+
+template <int EB>
+hipError_t launch_split_e(const pa_decode_params& p, int group, hipStream_t s) {
+    switch (group) {
+        case 1: return launch_split_g<EB, 1>(p, s);
+        case 2: return launch_split_g<EB, 2>(p, s);
+        case 4: return launch_split_g<EB, 4>(p, s);
+        case 8: return launch_split_g<EB, 8>(p, s);
+    }
+    throw std::invalid_argument("unsupported GQA group size " + std::to_string(group));
+}
+
+template <int G>
+hipError_t launch_merge_g(const pa_decode_params& p, hipStream_t s) {
+    const dim3 grid(p.num_q_heads, p.batch);
+    const int m = p.max_item_segments;
+    if (m > 0 && m <= 4)
+        hipLaunchKernelGGL((decode_merge_kernel<G, 1>), grid, dim3(64), 0, s, p);
+    else if (m > 0 && m <= 16)
+        hipLaunchKernelGGL((decode_merge_kernel<G, 4>), grid, dim3(256), 0, s, p);
+    else
+        hipLaunchKernelGGL((decode_merge_kernel<G, 16>), grid, dim3(1024), 0, s, p);
+    return hipGetLastError();
+}
+
+int checked_group(const pa_decode_params& p) {
+    if (p.head_dim != kHeadDim) throw std::invalid_argument("unsupported head_dim " + std::to_string(p.head_dim));
+    if (p.num_kv_heads <= 0 || p.num_q_heads % p.num_kv_heads != 0)
+        throw std::invalid_argument("num_q_heads must be a multiple of num_kv_heads");
+    const int g = p.num_q_heads / p.num_kv_heads;
+    if (g != 1 && g != 2 && g != 4 && g != 8)
+        throw std::invalid_argument("unsupported GQA group size " + std::to_string(g));
+    return g;
+}
+
+template <int EB, int G>
+const void* split_symbol() {
+    if constexpr (EB == 2)
+        return reinterpret_cast<const void*>(
+            &decode_split_kernel_f16<G, Tune<EB>::step, Tune<EB>::depth, kPagePow2>);
+    else
+        return reinterpret_cast<const void*>(
+            &decode_split_kernel_fp8<G, Tune<EB>::step, Tune<EB>::depth, kPagePow2>);
+}
+
+}  // namespace
+
+int kernel_tile_tokens(int dtype, int group) {
+    check_kv_dtype(dtype);
+    if (group != 1 && group != 2 && group != 4 && group != 8)
+        throw std::invalid_argument("unsupported GQA group size " + std::to_string(group));
+    return dtype == PA_KV_FP16 ? Tune<2>::step : Tune<1>::step;
+}
+
+int kernel_units_per_cu(int dtype, int group) {
+    check_kv_dtype(dtype);
+    const void* fn = nullptr;
+    const bool fp16 = dtype == PA_KV_FP16;
+    switch (group) {
+        case 1: fn = fp16 ? split_symbol<2, 1>() : split_symbol<1, 1>(); break;
+        case 2: fn = fp16 ? split_symbol<2, 2>() : split_symbol<1, 2>(); break;
+        case 4: fn = fp16 ? split_symbol<2, 4>() : split_symbol<1, 4>(); break;
+        case 8: fn = fp16 ? split_symbol<2, 8>() : split_symbol<1, 8>(); break;
+        default: throw std::invalid_argument("unsupported GQA group size " + std::to_string(group));
+    }
+    int blocks = 0;
+    hip_check(hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, fn, 64 * kWaves, 0),
+              "hipOccupancyMaxActiveBlocksPerMultiprocessor");
+    return blocks * kWaves;
+}
+
+hipError_t launch_decode_split(int dtype, const pa_decode_params& p, hipStream_t s) {
+    check_kv_dtype(dtype);
+    const int g = checked_group(p);
+    if (p.num_ctas <= 0) return hipSuccess;
+    if (p.page_size <= 0 || p.block_table_stride <= 0 || p.batch <= 0)
+        throw std::invalid_argument("decode: page_size, block_table_stride and batch must be positive");
+    if (!p.q || !p.out || !p.k_cache || !p.v_cache || !p.block_table || !p.segments || !p.cta_seg_begin ||
+        !p.item_seg_begin)
+        throw std::invalid_argument("decode: null pointer in params");
+    if (p.needs_merge && (!p.partial_out || !p.partial_lse))
+        throw std::invalid_argument("decode: split rows need the partial workspace");
+    return dtype == PA_KV_FP16 ? launch_split_e<2>(p, g, s) : launch_split_e<1>(p, g, s);
+}
+
+hipError_t launch_decode_merge(int dtype, const pa_decode_params& p, hipStream_t s) {
+    check_kv_dtype(dtype);
+    const int g = checked_group(p);
+    if (!p.needs_merge || p.batch <= 0) return hipSuccess;
+    if (!p.partial_out || !p.partial_lse || !p.item_seg_begin || !p.out)
+        throw std::invalid_argument("decode merge: null pointer in params");
+    switch (g) {
+        case 1: return launch_merge_g<1>(p, s);
+        case 2: return launch_merge_g<2>(p, s);
+        case 4: return launch_merge_g<4>(p, s);
+        case 8: return launch_merge_g<8>(p, s);
+    }
+    return hipSuccess;
+}
+
+}  // namespace pa

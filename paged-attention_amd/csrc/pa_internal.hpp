@@ -26,6 +26,11 @@ inline void hip_check(hipError_t e, const char* what) {
 constexpr int kHeadDim     = 128;   // the only head_dim the path supports (decode.cu:31-38)
 constexpr int kGroupTokens = 16;    // tokens per MFMA step of the decode kernel
 
+inline void check_kv_dtype(int dtype) {
+    if (dtype != PA_KV_FP16 && dtype != PA_KV_FP8_E4M3)
+        throw std::invalid_argument("unknown kv dtype " + std::to_string(dtype));
+}
+
 // Tokens per planning tile (decode.cu:43-45 tile_tokens). The gfx950 kernel
 // consumes 16-token groups, so every 16-token boundary is a legal cut.
 int kernel_tile_tokens(int dtype, int group);
@@ -41,7 +46,7 @@ hipError_t launch_append(int dtype, const uint16_t* k, const uint16_t* v, void* 
                          int page_size, float inv_k, float inv_v, hipStream_t s);
 hipError_t launch_gather(int dtype, const void* cache, const int32_t* bt_row, int hkv,
                          int page_size, int kv_head, int len, void* out, hipStream_t s);
-hipError_t launch_stream_read(const void* buf, size_t bytes, int blocks, uint32_t* sink,
-                              hipStream_t s);
+hipError_t launch_stream_read(const void* buf, size_t bytes, int blocks, int threads, int unroll, bool nt,
+                              uint32_t* sink, hipStream_t s);
 
 }  // namespace pa

@@ -71,6 +71,7 @@ class DecodeParams(ctypes.Structure):
         ("needs_merge", ctypes.c_int32),
         ("partial_out", ctypes.c_void_p),
         ("partial_lse", ctypes.c_void_p),
+        ("max_item_segments", ctypes.c_int32),
     ]
 
 
@@ -124,6 +125,7 @@ SIGNATURES: dict[str, tuple] = {
     "pa_append_quantize": (_I, [_I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _F, _P]),
     "pa_gather_kv": (_I, [_I, _P, _P, _I, _I, _I, _I, _I, _P, _P]),
     "pa_stream_read": (_I, [_P, _S, _I, _P, _P]),
+    "pa_stream_read_ex": (_I, [_P, _S, _I, _I, _I, _I, _P, _P]),
     "pa_pool_create": (_I, [_I, _I, _I, _I, _PP]),
     "pa_pool_destroy": (None, [_P]),
     "pa_pool_admit": (_I, [_P]),

@@ -1,0 +1,316 @@
+"""Benchmarks of the paged split-KV decode path; CSV on stdout, the same modes,
+flags and columns as the reference's bench/bench_decode.cu:1-16:
+
+    python -m pa_amd.bench_decode sweep     [--dtype fp16|fp8]   batch x seq_len sweep
+    python -m pa_amd.bench_decode ctas      --batch B --len L     persistent-grid sweep
+    python -m pa_amd.bench_decode pagesize  --batch B --len L     page-size sweep
+    python -m pa_amd.bench_decode capacity  [--budget-gib G]     sequences per KV budget
+    python -m pa_amd.bench_decode copy                           attainable read bandwidth
+    python -m pa_amd.bench_decode single    --batch B --len L    one configuration
+
+Common flags: --hq 32 --hkv 8 --dim 128 --page 16 --iters 50 --dtype fp16|fp8
+              --ctas N (0 = default grid) --contiguous-pages (no free-list shuffle)
+              --peak-gbps X (default 8000, MI355X HBM3E)
+              --warm (no cache flush between iterations: what a working set that
+                      fits the 256 MiB Infinity Cache costs when it is resident)
+
+Timing (bench_decode.cu:120-139): the step is planned once; every iteration
+first streams a 1 GiB buffer (larger than L2 plus the 256 MiB Infinity Cache,
+where the reference's 2 x L2 would not be) so the KV cache is read from HBM,
+then times only the decode kernels with HIP events; the median is reported.
+Bandwidth counts the bytes the kernel must move (bench_decode.cu:186-191).
+
+Data: q/K/V ~ N(0,1) rounded to fp16, distinct per sequence, appended through
+PagedKVCache.append (FP8: per-tensor amax/448 scales, quantized by the append
+kernel). The reference bench fills uniform [-2, 2] and appends one K/V to every
+sequence; the values do not change the timing.
+"""
+
+from __future__ import annotations
+
+import math
+import statistics
+import sys
+
+import numpy as np
+
+from . import core
+
+PEAK_GBPS = 8000.0
+FLUSH_BYTES = 1 << 30
+
+
+def algorithmic_bytes(lens, hq: int, hkv: int, dim: int, page: int, fp8: bool) -> int:
+    """bench_decode.cu:186-191: K and V once, q in and out once, the block table."""
+    e = 1 if fp8 else 2
+    return (2 * sum(lens) * hkv * dim * e + 2 * len(lens) * hq * dim * 2
+            + sum(math.ceil(L / page) for L in lens) * 4)
+
+
+class Setup:
+    """A populated PagedKVCache plus q/out and a bound plan for one decode shape
+    (bench_decode.cu:142-192)."""
+
+    def __init__(self, lens, hq: int = 32, hkv: int = 8, dim: int = 128, page: int = 16,
+                 fp8: bool = False, shuffle: bool = True, ctas: int = 0, seed: int = 42,
+                 k_scale: float | None = None, v_scale: float | None = None):
+        import torch
+
+        self.lens = [int(x) for x in lens]
+        self.batch = len(self.lens)
+        self.hq, self.hkv, self.dim, self.page, self.fp8 = hq, hkv, dim, page, fp8
+        self.dtype = core.FP8_E4M3 if fp8 else core.FP16
+        pages = [math.ceil(L / page) for L in self.lens]
+        self.num_pages = sum(pages)
+        g = torch.Generator(device="cuda").manual_seed(seed)
+        stream = torch.cuda.current_stream()
+        srcs = [(torch.randn(L, hkv, dim, device="cuda", dtype=torch.float16, generator=g),
+                 torch.randn(L, hkv, dim, device="cuda", dtype=torch.float16, generator=g)) for L in self.lens]
+        if fp8:
+            self.k_scale = k_scale or max(float(k.abs().max()) for k, _ in srcs) / 448.0
+            self.v_scale = v_scale or max(float(v.abs().max()) for _, v in srcs) / 448.0
+        else:
+            self.k_scale = self.v_scale = 1.0
+        self.cache = core.PagedKVCache(self.num_pages, page, hkv, dim, self.batch, max(pages), self.dtype,
+                                       self.k_scale, self.v_scale)
+        if shuffle:
+            self.cache.shuffle_free_pages(seed)
+        for b, (k, v) in enumerate(srcs):
+            slot = self.cache.admit()
+            assert slot == b
+            if not self.cache.append(slot, k, v, self.lens[b], stream):
+                raise RuntimeError("setup: out of pages")
+        del srcs
+        self.q = torch.randn(self.batch, hq, dim, device="cuda", dtype=torch.float16, generator=g)
+        self.out = torch.empty_like(self.q)
+        self.dplan = core.DevicePlan()
+        self.replan(ctas)
+        torch.cuda.synchronize()
+
+    def replan(self, ctas: int) -> None:
+        """PagedKVCache::plan with slots 0..B-1 (bench_decode.cu:198-201)."""
+        import ctypes
+        import torch
+        self.plan = core.make_plan(self.dtype, self.lens, self.hq, self.hkv, self.dim, ctas)
+        self.dplan.upload(self.plan, self.hq // self.hkv, self.dim, torch.cuda.current_stream())
+        p = self.cache.params()
+        p.q = self.q.data_ptr()
+        p.out = self.out.data_ptr()
+        p.slot_ids = None   # slot b holds row b
+        p.batch = self.batch
+        p.num_q_heads = self.hq
+        self.dplan.bind(p)
+        self.params = p
+        self._lib = core.load()
+        self._pref = ctypes.byref(self.params)
+
+    def bytes(self) -> int:
+        return algorithmic_bytes(self.lens, self.hq, self.hkv, self.dim, self.page, self.fp8)
+
+    # The two launches of one decode step on a raw hipStream_t handle.
+    def split(self, sh: int) -> None:
+        core.check(self._lib.pa_decode_split(self.dtype, self._pref, sh))
+
+    def merge(self, sh: int) -> None:
+        core.check(self._lib.pa_decode_merge(self.dtype, self._pref, sh))
+
+    def run(self, sh: int) -> None:
+        core.check(self._lib.pa_decode(self.dtype, self._pref, sh))
+
+    def close(self) -> None:
+        self.cache.close()
+
+
+class Flusher:
+    """Streams FLUSH_BYTES so the next kernel reads from HBM (bench_decode.cu:105-117)."""
+
+    def __init__(self, nbytes: int = FLUSH_BYTES):
+        import torch
+        self.buf = torch.ones(nbytes, dtype=torch.uint8, device="cuda")
+        self.sink = torch.zeros(1, dtype=torch.int32, device="cuda")
+
+    def flush(self, stream) -> None:
+        core.stream_read(self.buf, self.buf.numel(), 2048, self.sink, stream)
+
+
+def time_cold(flusher: Flusher | None, iters: int, fn) -> list[float]:
+    """bench_decode.cu:120-139: 5 flushed warm-ups, then per iteration flush,
+    event, fn, event. Returns the per-iteration milliseconds. flusher=None
+    times warm (no flush)."""
+    import torch
+    stream = torch.cuda.current_stream()
+    sh = stream.cuda_stream
+    for _ in range(5):
+        if flusher:
+            flusher.flush(stream)
+        fn(sh)
+    ms = []
+    for _ in range(iters):
+        if flusher:
+            flusher.flush(stream)
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        fn(sh)
+        b.record(stream)
+        b.synchronize()
+        ms.append(a.elapsed_time(b))
+    return ms
+
+
+def copy_rows(cus: int, iters: int = 10, nbytes: int = 4 << 30) -> list[dict]:
+    """bench_decode.cu:224-240 plus unrolled and non-temporal variants of the
+    same 16 B/lane read: one row per (grid, block, unroll, nt)."""
+    import torch
+    buf = torch.ones(nbytes, dtype=torch.uint8, device="cuda")
+    sink = torch.zeros(1, dtype=torch.int32, device="cuda")
+    stream = torch.cuda.current_stream()
+    rows = []
+    variants = [(m, 512, 1, False) for m in (4, 8, 16, 32)]
+    variants += [(m, 256, u, nt) for m in (4, 8, 16) for u in (4, 8) for nt in (False, True)]
+    for mult, threads, unroll, nt in variants:
+        blocks = cus * mult
+        ms = []
+        for i in range(iters + 2):
+            a = torch.cuda.Event(enable_timing=True)
+            b = torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            core.stream_read(buf, nbytes, blocks, sink, stream, threads=threads, unroll=unroll, nontemporal=nt)
+            b.record(stream)
+            b.synchronize()
+            if i >= 2:
+                ms.append(a.elapsed_time(b))
+        med = statistics.median(ms)
+        rows.append({"kernel": f"read_{blocks}x{threads}_u{unroll}{'_nt' if nt else ''}", "bytes": nbytes,
+                     "time_us": med * 1e3, "gbps": nbytes / (med * 1e-3) / 1e9})
+    del buf
+    return rows
+
+
+# ---- CLI (bench_decode.cu:213-326) ------------------------------------------
+
+HEADER = "gpu,dtype,batch,seq_len,hq,hkv,dim,page,ctas,segments,time_us,gbps,pct_peak"
+
+SWEEP_SHAPES = [(1, 4096), (1, 16384), (1, 65536), (1, 131072), (8, 4096), (8, 16384), (8, 32768),
+                (32, 1024), (32, 4096), (32, 8192), (64, 1024), (64, 4096), (128, 1024), (128, 2048)]
+
+
+def _parse(argv: list[str]):
+    mode = "sweep"
+    kv: dict[str, str] = {}
+    i = 0
+    if argv and not argv[0].startswith("-"):
+        mode = argv[0]
+        i = 1
+    while i < len(argv):
+        k = argv[i]
+        if k.startswith("--"):
+            if i + 1 < len(argv) and not argv[i + 1].startswith("--"):
+                kv[k[2:]] = argv[i + 1]
+                i += 1
+            else:
+                kv[k[2:]] = "1"
+        i += 1
+    return mode, kv
+
+
+def run_one(gpu: str, peak: float, fl: Flusher | None, s: Setup, ctas: int, iters: int) -> dict:
+    s.replan(ctas)
+    ms = statistics.median(time_cold(fl, iters, s.run))
+    gbps = s.bytes() / (ms * 1e-3) / 1e9
+    row = dict(gpu=gpu, dtype=core.kv_dtype_name(s.dtype), batch=s.batch, seq_len=max(s.lens), hq=s.hq,
+               hkv=s.hkv, dim=s.dim, page=s.page, ctas=s.plan.num_ctas, segments=len(s.plan.segments),
+               time_us=ms * 1e3, gbps=gbps, pct_peak=100.0 * gbps / peak)
+    print(f"{gpu},{row['dtype']},{s.batch},{row['seq_len']},{s.hq},{s.hkv},{s.dim},{s.page},{row['ctas']},"
+          f"{row['segments']},{row['time_us']:.2f},{gbps:.1f},{row['pct_peak']:.1f}", flush=True)
+    return row
+
+
+def main(argv: list[str] | None = None) -> int:
+    import torch
+    mode, a = _parse(sys.argv[1:] if argv is None else argv)
+    geti = lambda k, d: int(a.get(k, d))   # noqa: E731
+    core.load()
+    props = torch.cuda.get_device_properties(0)
+    gpu = props.name.replace(",", " ")
+    cus = props.multi_processor_count
+    peak = float(a.get("peak-gbps", PEAK_GBPS))
+    print(f"# {gpu}, {cus} CUs, HBM peak {peak:.0f} GB/s", file=sys.stderr, flush=True)
+    hq, hkv, dim = geti("hq", 32), geti("hkv", 8), geti("dim", 128)
+    page, iters, ctas = geti("page", 16), geti("iters", 50), geti("ctas", 0)
+    shuffle = "contiguous-pages" not in a
+
+    if mode == "copy":
+        print("gpu,kernel,bytes,time_us,gbps,pct_peak")
+        for r in copy_rows(cus):
+            print(f"{gpu},{r['kernel']},{r['bytes']},{r['time_us']:.2f},{r['gbps']:.1f},"
+                  f"{100 * r['gbps'] / peak:.1f}", flush=True)
+        return 0
+
+    fl = None if "warm" in a else Flusher()
+    fp8 = a.get("dtype", "fp16") == "fp8"
+    if mode == "sweep":
+        print(HEADER)
+        dts = [fp8] if "dtype" in a else [False, True]
+        for dt in dts:
+            for b, L in SWEEP_SHAPES:
+                s = Setup([L] * b, hq, hkv, dim, page, dt, shuffle)
+                run_one(gpu, peak, fl, s, ctas, iters)
+                s.close()
+        return 0
+
+    batch, length = geti("batch", 32), geti("len", 4096)
+    if mode == "single":
+        print(HEADER)
+        s = Setup([length] * batch, hq, hkv, dim, page, fp8, shuffle)
+        run_one(gpu, peak, fl, s, ctas, iters)
+        return 0
+    if mode == "ctas":
+        print(HEADER)
+        s = Setup([length] * batch, hq, hkv, dim, page, fp8, shuffle)
+        wave = core.wave_ctas(s.dtype, dim, hq // hkv)
+        print(f"# one wave = {wave} work units", file=sys.stderr, flush=True)
+        grid = [cus // 2, cus, 2 * cus, 3 * cus, 4 * cus, 6 * cus, 8 * cus, 12 * cus, 16 * cus, wave]
+        for n in sorted(set(grid)):
+            run_one(gpu, peak, fl, s, n, iters)
+        return 0
+    if mode == "pagesize":
+        print(HEADER)
+        for ps in (1, 4, 8, 16, 32, 64, 128, 256, 1024, length):
+            if ps > length:
+                continue
+            s = Setup([length] * batch, hq, hkv, dim, ps, fp8, shuffle)
+            run_one(gpu, peak, fl, s, ctas, iters)
+            s.close()
+        return 0
+    if mode == "capacity":
+        # bench_decode.cu:285-321: sequences that fit one layer's KV budget.
+        budget = int(float(a.get("budget-gib", 1.0)) * (1 << 30))
+        max_len = geti("max-len", 8192)
+        print("dtype,layout,max_len,actual_len,sequences,bytes_per_seq")
+        for actual in (256, 512, 1024, 2048, 4096, 8192):
+            per_contig = 2 * max_len * hkv * dim * 2
+            print(f"fp16,contiguous,{max_len},{actual},{budget // per_contig},{per_contig}")
+            for dt in (core.FP16, core.FP8_E4M3):
+                cfg = core.CacheConfig(0, page, hkv, dim, 0, (max_len + page - 1) // page, dt,
+                                       2.0 / 448.0, 2.0 / 448.0)
+                n_pages = core.PagedKVCache.pages_for_budget(cfg, budget)
+                cache = core.PagedKVCache(n_pages, page, hkv, dim, n_pages, (max_len + page - 1) // page, dt,
+                                          2.0 / 448.0, 2.0 / 448.0)
+                src = (torch.rand(actual, hkv, dim, device="cuda") * 4 - 2).to(torch.float16)
+                n = 0
+                while True:
+                    slot = cache.admit()
+                    if slot < 0 or not cache.append(slot, src, src, actual):
+                        break
+                    n += 1
+                print(f"{core.kv_dtype_name(dt)},paged,{max_len},{actual},{n},"
+                      f"{cache.total_bytes() // n if n else 0}", flush=True)
+                cache.close()
+        return 0
+    print(f"unknown mode {mode}", file=sys.stderr)
+    return 1
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -191,8 +191,11 @@ def gather_kv(dtype: int, cache, block_table_row, num_kv_heads: int, head_dim: i
          page_size, kv_head, length, _ptr(out), _stream(stream))
 
 
-def stream_read(buf, nbytes: int, blocks: int, sink, stream=None) -> None:
-    call("pa_stream_read", _ptr(buf), nbytes, blocks, _ptr(sink), _stream(stream))
+def stream_read(buf, nbytes: int, blocks: int, sink, stream=None, threads: int = 256, unroll: int = 1,
+                nontemporal: bool = False) -> None:
+    """bench_decode.cu:70-78 read_kernel (threads=256, unroll=1) and its unrolled variants."""
+    call("pa_stream_read_ex", _ptr(buf), nbytes, blocks, threads, unroll, int(nontemporal), _ptr(sink),
+         _stream(stream))
 
 
 class PagePool:
