@@ -25,6 +25,11 @@ Fields of the JSON line:
                oracle/_ref when that exists, else the oracle's restatement)
                over every (row, query head) pair of the same workload, K/V
                gathered and dequantized to fp32 beforehand (untimed)
+  roofline.traffic  HBM bytes per split-kernel launch from two rocprofv3
+               counter passes run as child processes before this process
+               touches the GPU (FETCH_SIZE, then WRITE_SIZE, in KiB per
+               dispatch), each scaled by what the same counter reads for a
+               read kernel and a write kernel of known size in the same run
 
 Multi-GPU runs are not part of this build: --gpus > 1 exits with a message.
 """
@@ -157,6 +162,74 @@ def time_steps(s, steps: int, warmup: int):
     return wall, [a.elapsed_time(b) for a, b in ev]
 
 
+CALIB_BYTES = 1 << 30   # size of the counter-calibration read and write kernels
+
+
+def pmc_child(args) -> None:
+    """Runs under rocprofv3 --pmc: a read and a write of CALIB_BYTES each (the
+    counters' calibration), then a few decode steps of the workload."""
+    import torch
+    from pa_amd import bench_decode as bd
+    import pa_amd
+    torch.cuda.set_device(0)
+    pa_amd._lib.load()
+    desc, _, _, _, fp8 = CONFIGS[args.config]
+    s = bd.Setup(seq_lens_of(args.config), HQ, HKV, D, args.page_size, fp8, shuffle=True, ctas=args.ctas)
+    buf = torch.empty(CALIB_BYTES, dtype=torch.uint8, device="cuda")
+    sink = torch.zeros(1, dtype=torch.int32, device="cuda")
+    pa_amd.fill_bytes(buf, CALIB_BYTES, 1)
+    pa_amd.stream_read(buf, CALIB_BYTES, 2048, sink, threads=256, unroll=8, nontemporal=True)
+    sh = torch.cuda.current_stream().cuda_stream
+    for _ in range(3):
+        s.split(sh)
+        s.merge(sh)
+    torch.cuda.synchronize()
+    s.close()
+
+
+def measure_traffic(args) -> dict | None:
+    """Two rocprofv3 counter passes over pmc_child; returns the split kernel's
+    HBM bytes per launch (read, written, total) and the calibration factors,
+    or None if the profiler is unavailable or a pass fails."""
+    import csv
+    import shutil
+    import subprocess
+    import tempfile
+    prof = shutil.which("rocprofv3")
+    if not prof:
+        return None
+    out = {}
+    with tempfile.TemporaryDirectory(prefix="pa_pmc_") as tmp:
+        for counter, calib in (("FETCH_SIZE", "stream_read_kernel"), ("WRITE_SIZE", "fill_bytes_kernel")):
+            d = pathlib.Path(tmp) / counter
+            cmd = [prof, "--pmc", counter, "-d", str(d), "-o", "run", "--output-format", "csv", "--",
+                   sys.executable, str(ROOT / "bench.py"), "--pmc-child", "--config", args.config,
+                   "--page-size", str(args.page_size), "--ctas", str(args.ctas)]
+            print(f"# traffic pass: {counter}", file=sys.stderr, flush=True)
+            try:
+                subprocess.run(cmd, stdout=subprocess.DEVNULL, stderr=subprocess.DEVNULL, timeout=180, check=False)
+            except subprocess.TimeoutExpired:
+                return None
+            files = list(d.rglob("*counter_collection.csv"))
+            if not files:
+                return None
+            split, cal = [], []
+            with open(files[0]) as f:
+                for r in csv.DictReader(f):
+                    if r.get("Counter_Name") != counter:
+                        continue
+                    if "decode_split_kernel" in r["Kernel_Name"]:
+                        split.append(float(r["Counter_Value"]))
+                    elif calib in r["Kernel_Name"]:
+                        cal.append(float(r["Counter_Value"]))
+            if not split or not cal or cal[0] <= 0:
+                return None
+            factor = CALIB_BYTES / (statistics.mean(cal) * 1024.0)   # true bytes per counted byte
+            out[counter] = {"kib_per_dispatch": statistics.mean(split), "factor": factor,
+                            "bytes": statistics.mean(split) * 1024.0 * factor}
+    return out
+
+
 def _barrier() -> None:
     import torch.distributed as dist
     if dist.is_available() and dist.is_initialized():
@@ -177,12 +250,21 @@ def main() -> None:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-cold", action="store_true")
     ap.add_argument("--no-copy", action="store_true")
+    ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 counter passes")
+    ap.add_argument("--pmc-child", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
+
+    if args.pmc_child:
+        pmc_child(args)
+        return
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only; multi-GPU runs (--gpus > 1) are not part of it",
               file=sys.stderr)
         sys.exit(2)
+
+    # The counter passes run before this process initializes the GPU.
+    traffic = None if args.no_traffic else measure_traffic(args)
 
     import torch
     if not torch.cuda.is_available():
@@ -250,6 +332,15 @@ def main() -> None:
             "avg_us": round(split_avg * 1e3, 2),
         },
     }
+    if traffic:
+        rd, wr = traffic["FETCH_SIZE"], traffic["WRITE_SIZE"]
+        result["roofline"]["traffic"] = int(rd["bytes"] + wr["bytes"])
+        result["roofline"]["traffic_detail"] = {
+            "read_bytes": int(rd["bytes"]), "write_bytes": int(wr["bytes"]),
+            "fetch_kib_per_dispatch": round(rd["kib_per_dispatch"], 1),
+            "write_kib_per_dispatch": round(wr["kib_per_dispatch"], 1),
+            "fetch_factor": round(rd["factor"], 4), "write_factor": round(wr["factor"], 4),
+            "vs_algorithmic": round((rd["bytes"] + wr["bytes"]) / nbytes, 4)}
 
     if not args.no_copy:
         rows = bd.copy_rows(cus)

@@ -165,6 +165,11 @@ pa_status pa_stream_read(const void* buf, size_t bytes, int blocks, uint32_t* si
 pa_status pa_stream_read_ex(const void* buf, size_t bytes, int blocks, int threads_per_block, int unroll,
                             int nontemporal, uint32_t* sink, void* stream);
 
+/* Streaming write of the byte `value` over `bytes` (a multiple of 16): the
+ * write-side counterpart of pa_stream_read (bench_decode.cu:61-68 fills the
+ * bench inputs; here it is a write of known size for counter calibration). */
+pa_status pa_fill_bytes(void* buf, size_t bytes, int value, void* stream);
+
 /* ---- host page pool (paged_kv_cache.cu:84-151, no device memory) -------- */
 
 typedef struct pa_pool pa_pool;

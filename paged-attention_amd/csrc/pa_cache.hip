@@ -3,6 +3,8 @@
 //   append_kernel        fp16 copy / FP8 E4M3 quantize + page scatter (paged_kv_cache.cu:15-39)
 //   gather_kernel        block-table resolution probe (the decode kernel's row address function)
 //   stream_read_kernel   streaming read: cache flush and plain-copy ceiling (bench_decode.cu:70-78)
+//   fill_bytes_kernel    streaming write of a byte value (bench_decode.cu:61-68's fill role; the
+//                        write-side counterpart of the copy ceiling)
 
 #include "pa_device.hpp"
 
@@ -118,6 +120,13 @@ __global__ __launch_bounds__(512) void stream_read_kernel(const u32x4* __restric
     if (acc == 0x12345678u) *sink = acc;   // keeps the loads alive
 }
 
+// Streaming write: every 16-byte word of x gets `word` repeated.
+__global__ __launch_bounds__(256) void fill_bytes_kernel(u32x4* __restrict__ x, size_t n, uint32_t word) {
+    const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+    for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride)
+        x[i] = u32x4{word, word, word, word};
+}
+
 }  // namespace
 
 hipError_t launch_append(int dtype, const uint16_t* k, const uint16_t* v, void* k_cache, void* v_cache,
@@ -147,6 +156,17 @@ hipError_t launch_gather(int dtype, const void* cache, const int32_t* bt_row, in
     else
         hipLaunchKernelGGL(gather_kernel<1>, dim3(blocks), dim3(256), 0, s, cache, bt_row, hkv, page_size, kv_head,
                            len, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_fill_bytes(void* buf, size_t bytes, int value, hipStream_t s) {
+    const size_t n = bytes / 16;
+    if (n == 0) return hipSuccess;
+    const uint32_t b = static_cast<uint32_t>(value) & 0xffu;
+    const size_t want = (n + 255) / 256;
+    const int blocks = static_cast<int>(want < 16384 ? want : 16384);
+    hipLaunchKernelGGL(fill_bytes_kernel, dim3(blocks), dim3(256), 0, s, static_cast<u32x4*>(buf), n,
+                       b | (b << 8) | (b << 16) | (b << 24));
     return hipGetLastError();
 }
 

@@ -523,6 +523,13 @@ pa_status pa_stream_read_ex(const void* buf, size_t bytes, int blocks, int threa
     });
 }
 
+pa_status pa_fill_bytes(void* buf, size_t bytes, int value, void* stream) {
+    return guarded([&] {
+        if (bytes % 16 != 0 || (bytes && !buf)) throw std::invalid_argument("fill_bytes: bad arguments");
+        pa::hip_check(pa::launch_fill_bytes(buf, bytes, value, as_stream(stream)), "fill kernel launch");
+    });
+}
+
 // ---- pool
 
 pa_status pa_pool_create(int num_pages, int page_size, int max_slots, int max_pages_per_slot, pa_pool** out) {

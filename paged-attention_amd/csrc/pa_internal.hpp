@@ -46,6 +46,7 @@ hipError_t launch_append(int dtype, const uint16_t* k, const uint16_t* v, void* 
                          int page_size, float inv_k, float inv_v, hipStream_t s);
 hipError_t launch_gather(int dtype, const void* cache, const int32_t* bt_row, int hkv,
                          int page_size, int kv_head, int len, void* out, hipStream_t s);
+hipError_t launch_fill_bytes(void* buf, size_t bytes, int value, hipStream_t s);
 hipError_t launch_stream_read(const void* buf, size_t bytes, int blocks, int threads, int unroll, bool nt,
                               uint32_t* sink, hipStream_t s);
 

@@ -198,6 +198,11 @@ def stream_read(buf, nbytes: int, blocks: int, sink, stream=None, threads: int =
          _stream(stream))
 
 
+def fill_bytes(buf, nbytes: int, value: int, stream=None) -> None:
+    """Streaming write of one byte value (a write of known size)."""
+    call("pa_fill_bytes", _ptr(buf), nbytes, value, _stream(stream))
+
+
 class PagePool:
     """Host page allocator + block tables (paged_kv_cache.cu:84-151), no device memory."""
 
@@ -347,6 +352,6 @@ def sm_scale(head_dim: int) -> float:
 __all__ = [
     "FP16", "FP8_E4M3", "DecodeParams", "CacheConfig", "DecodePlan", "DevicePlan", "PagePool",
     "PagedKVCache", "make_plan", "make_plan_tiled", "paged_decode", "decode_split", "decode_merge",
-    "append_quantize", "gather_kv", "stream_read", "tile_tokens", "wave_ctas", "default_ctas",
+    "append_quantize", "gather_kv", "stream_read", "fill_bytes", "tile_tokens", "wave_ctas", "default_ctas",
     "kv_dtype_bytes", "kv_dtype_name", "sm_scale",
 ]
