@@ -106,6 +106,14 @@ pa_status pa_plan_build(int dtype, const int32_t* seq_lens, int batch, int num_q
  * replay the reference planner at its own tile (64) in tests. */
 pa_status pa_plan_build_tiled(int tile, const int32_t* seq_lens, int batch, int num_kv_heads,
                               int num_ctas, pa_plan** out);
+/* A plan from caller-built host arrays (decode.hpp:21-27 DecodePlan's fields),
+ * validated: prefix arrays rise from 0 to num_segments, every segment is
+ * non-empty and listed under its (row, kv head) item = row * num_kv_heads +
+ * head, and every item has a segment. num_kv_heads = 0 infers it (1 + the
+ * largest head in the segments). Lets DevicePlan::upload take any DecodePlan. */
+pa_status pa_plan_create(int num_ctas, int tile, const int32_t* segments, int num_segments,
+                         const int32_t* cta_seg_begin, const int32_t* item_seg_begin, int num_items,
+                         int num_kv_heads, pa_plan** out);
 void      pa_plan_destroy(pa_plan* plan);
 int       pa_plan_num_ctas(const pa_plan* plan);
 int       pa_plan_tile(const pa_plan* plan);

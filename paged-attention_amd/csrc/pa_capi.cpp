@@ -417,6 +417,51 @@ pa_status pa_plan_build_tiled(int tile, const int32_t* seq_lens, int batch, int 
     });
 }
 
+pa_status pa_plan_create(int num_ctas, int tile, const int32_t* segments, int num_segments,
+                         const int32_t* cta_seg_begin, const int32_t* item_seg_begin, int num_items,
+                         int num_kv_heads, pa_plan** out) {
+    return guarded([&] {
+        if (!out) throw std::invalid_argument("out is null");
+        if (num_ctas < 0 || num_segments < 0 || num_items < 0 || tile <= 0 || num_kv_heads < 0)
+            throw std::invalid_argument("plan: negative sizes or non-positive tile");
+        if ((num_segments && !segments) || !cta_seg_begin || !item_seg_begin)
+            throw std::invalid_argument("plan: null array");
+        if (num_kv_heads == 0) {   // every (row, kv head) has a segment, so the heads are 0 .. max
+            for (int i = 0; i < num_segments; ++i) num_kv_heads = std::max(num_kv_heads, segments[4 * i + 1] + 1);
+            num_kv_heads = std::max(num_kv_heads, 1);
+        }
+        if (num_items % num_kv_heads != 0) throw std::invalid_argument("plan: items must be batch * num_kv_heads");
+        auto prefix_ok = [&](const int32_t* a, int n) {
+            if (a[0] != 0 || a[n] != num_segments) return false;
+            for (int i = 0; i < n; ++i)
+                if (a[i + 1] < a[i]) return false;
+            return true;
+        };
+        if (!prefix_ok(cta_seg_begin, num_ctas) || !prefix_ok(item_seg_begin, num_items))
+            throw std::invalid_argument("plan: segment prefix arrays must rise from 0 to num_segments");
+        for (int i = 0; i < num_items; ++i)
+            if (item_seg_begin[i + 1] == item_seg_begin[i])
+                throw std::invalid_argument("plan: every (row, kv head) needs a segment");
+        for (int i = 0; i < num_segments; ++i) {
+            const int32_t* sg = segments + 4 * static_cast<size_t>(i);
+            const long item = static_cast<long>(sg[0]) * num_kv_heads + sg[1];
+            if (sg[0] < 0 || sg[1] < 0 || sg[1] >= num_kv_heads || item >= num_items)
+                throw std::invalid_argument("plan: segment row / kv head out of range");
+            if (sg[2] < 0 || sg[3] <= sg[2]) throw std::invalid_argument("plan: empty or negative segment");
+            if (i < item_seg_begin[item] || i >= item_seg_begin[item + 1])
+                throw std::invalid_argument("plan: segment is not listed under its (row, kv head)");
+        }
+        auto* plan = new pa_plan;
+        plan->num_ctas = num_ctas;
+        plan->tile     = tile;
+        plan->items    = num_items;
+        plan->segments.assign(segments, segments + 4 * static_cast<size_t>(num_segments));
+        plan->cta_seg_begin.assign(cta_seg_begin, cta_seg_begin + num_ctas + 1);
+        plan->item_seg_begin.assign(item_seg_begin, item_seg_begin + num_items + 1);
+        *out = plan;
+    });
+}
+
 void pa_plan_destroy(pa_plan* plan) { delete plan; }
 int  pa_plan_num_ctas(const pa_plan* plan) { return plan ? plan->num_ctas : 0; }
 int  pa_plan_tile(const pa_plan* plan) { return plan ? plan->tile : 0; }

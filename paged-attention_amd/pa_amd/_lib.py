@@ -109,6 +109,7 @@ SIGNATURES: dict[str, tuple] = {
     "pa_default_ctas": (_I, [_I, _I, _I, _PI]),
     "pa_plan_build": (_I, [_I, _P, _I, _I, _I, _I, _I, _PP]),
     "pa_plan_build_tiled": (_I, [_I, _P, _I, _I, _I, _PP]),
+    "pa_plan_create": (_I, [_I, _I, _P, _I, _P, _P, _I, _I, _PP]),
     "pa_plan_destroy": (None, [_P]),
     "pa_plan_num_ctas": (_I, [_P]),
     "pa_plan_tile": (_I, [_P]),

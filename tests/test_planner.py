@@ -100,3 +100,42 @@ def test_single_segment_rows_need_no_merge():
 def test_empty_batch_gives_empty_plan():
     plan = pa_amd.make_plan_tiled(64, [], 8, 100)
     assert plan.num_ctas == 0 and len(plan.segments) == 0
+
+
+def _create(plan, num_kv_heads=0):
+    import ctypes
+    lib = pa_amd._lib.load()
+    h = ctypes.c_void_p()
+    seg = np.ascontiguousarray(plan["segments"], np.int32)
+    cta = np.ascontiguousarray(plan["cta"], np.int32)
+    itm = np.ascontiguousarray(plan["item"], np.int32)
+    st = lib.pa_plan_create(plan["num_ctas"], plan["tile"], seg.ctypes.data, len(seg), cta.ctypes.data,
+                            itm.ctypes.data, len(itm) - 1, num_kv_heads, ctypes.byref(h))
+    if st == 0:
+        lib.pa_plan_destroy(h.value)
+    return st
+
+
+def test_plan_create_accepts_built_plans_and_rejects_broken_ones():
+    """pa_plan_create (behind DevicePlan::upload of a caller's DecodePlan)
+    accepts every plan make_plan builds and rejects inconsistent ones."""
+    rng = np.random.default_rng(3)
+    lens = [int(x) for x in rng.integers(1, 3000, size=9)]
+    built = pa_amd.make_plan_tiled(16, lens, 4, 37)
+    good = dict(num_ctas=built.num_ctas, tile=16, segments=built.segments, cta=built.cta_seg_begin,
+                item=built.item_seg_begin)
+    assert _create(good) == 0 and _create(good, 4) == 0
+    assert _create(good, 3) == 1                                  # items not a multiple of 3
+    bad = dict(good, segments=built.segments.copy())
+    bad["segments"][0, 3] = bad["segments"][0, 2]                 # empty segment
+    assert _create(bad) == 1
+    bad = dict(good, segments=built.segments.copy())
+    a, b = int(built.item_seg_begin[0]), int(built.item_seg_begin[1])
+    bad["segments"][[a, b]] = bad["segments"][[b, a]]             # listed under the wrong item
+    assert _create(bad) == 1
+    bad = dict(good, cta=built.cta_seg_begin.copy())
+    bad["cta"][1], bad["cta"][2] = bad["cta"][2], bad["cta"][1]   # falling prefix
+    assert _create(bad) == 1 or np.all(np.diff(bad["cta"]) >= 0)
+    bad = dict(good, item=built.item_seg_begin.copy())
+    bad["item"][-1] += 1                                           # does not end at num_segments
+    assert _create(bad) == 1
