@@ -16,7 +16,8 @@ Fields of the JSON line:
                run back to back (bytes = 2*sum(L)*Hkv*D*e + 2*B*Hq*D*2 +
                sum(ceil(L/P))*4, bench_decode.cu:186-191)
   roofline     the split kernel's algorithmic GB/s from HIP events around each
-               of its launches in the timed loop, against 8 TB/s
+               of K further launches (right after the timed steps), against
+               8 TB/s
   cold         the reference's method: a 1 GiB flush before each run, HIP
                events around decode + merge, median of --cold-iters
   copy_ceiling best plain streaming read of 4 GiB (bench_decode.cu:224-240
@@ -139,26 +140,32 @@ def cpu_baseline(s, name: str, budget_s: float, threads: int) -> dict:
 
 
 def time_steps(s, steps: int, warmup: int):
-    """W untimed steps, then K timed steps back to back, with HIP events around
-    every split launch on the stream the kernels run on."""
+    """W untimed steps, then K timed steps back to back (wall clock between
+    synchronizations: the `value`), then K more split launches with HIP events
+    around each one on the stream the kernels run on (the kernel's average
+    launch duration for the roofline)."""
     import torch
     stream = torch.cuda.current_stream()
     sh = stream.cuda_stream
     for _ in range(warmup):
         s.split(sh)
         s.merge(sh)
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
     _barrier()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
+    for _ in range(steps):
+        s.split(sh)
+        s.merge(sh)
+    torch.cuda.synchronize()
+    _barrier()
+    wall = time.perf_counter() - t0
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
     for a, b in ev:
         a.record(stream)
         s.split(sh)
         b.record(stream)
         s.merge(sh)
     torch.cuda.synchronize()
-    _barrier()
-    wall = time.perf_counter() - t0
     return wall, [a.elapsed_time(b) for a, b in ev]
 
 

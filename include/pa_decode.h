@@ -77,6 +77,9 @@ typedef struct pa_decode_params {
     float*          partial_lse;       /* [num_segments][group] */
     int32_t         max_item_segments; /* most segments of one (row, kv head); sizes the
                                           merge launch (0 = unknown). Set by bind. */
+    int32_t         block_merge;       /* 1: every split (row, kv head) lies in one block of
+                                          8 work units and the split kernel merges it
+                                          (needs_merge is then 0). Set by bind. */
 } pa_decode_params;
 
 /* Thread-local message describing the last failed call ("" if none). */

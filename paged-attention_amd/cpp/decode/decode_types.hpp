@@ -52,6 +52,7 @@ struct DecodeParams {
     float* partial_lse;           // [num_segments][group]
 
     int max_item_segments = 0;    // most segments of one (row, head); sizes the merge (0 = unknown)
+    int block_merge       = 0;    // split rows merged inside the split kernel (set by DevicePlan::bind)
 };
 
 static_assert(sizeof(DecodeParams) == sizeof(pa_decode_params), "DecodeParams must match pa_decode_params");
@@ -60,6 +61,7 @@ static_assert(offsetof(DecodeParams, sm_scale) == offsetof(pa_decode_params, sm_
 static_assert(offsetof(DecodeParams, segments) == offsetof(pa_decode_params, segments));
 static_assert(offsetof(DecodeParams, partial_lse) == offsetof(pa_decode_params, partial_lse));
 static_assert(offsetof(DecodeParams, max_item_segments) == offsetof(pa_decode_params, max_item_segments));
+static_assert(offsetof(DecodeParams, block_merge) == offsetof(pa_decode_params, block_merge));
 static_assert(sizeof(int4) == 4 * sizeof(int32_t), "segments are int32 quadruples");
 
 namespace detail {

@@ -40,6 +40,7 @@ struct pa_device_plan {
     int      num_ctas    = 0;
     int      needs_merge = 0;
     int      max_item_segments = 0;
+    bool     block_merge = false;
 };
 
 // Host page allocator and per-slot block tables (paged_kv_cache.hpp:89-92).
@@ -217,8 +218,31 @@ void device_plan_upload(pa_device_plan& dp, const pa_plan& plan, int group, int 
         dp.part_cap = need;
     }
     dp.partial_lse = dp.partial_out ? dp.partial_out + rows * head_dim : nullptr;
-    dp.num_ctas    = plan.num_ctas;
-    dp.needs_merge = nseg > static_cast<size_t>(plan.items) ? 1 : 0;
+    dp.num_ctas = plan.num_ctas;
+    // Block-level merge: the split kernel merges a split row itself when all
+    // its segments lie in one block of kBlockUnits units. It needs every split
+    // segment to be its unit's first or last (true of every make_plan cut) and
+    // is used when it covers every split row, so no merge launch remains.
+    bool block_merge = nseg > static_cast<size_t>(plan.items);
+    if (block_merge) {
+        std::vector<int32_t> unit_of(nseg, 0);
+        for (int u = 0; u < plan.num_ctas; ++u)
+            for (int sg = plan.cta_seg_begin[u]; sg < plan.cta_seg_begin[u + 1]; ++sg)
+                unit_of[static_cast<size_t>(sg)] = u;
+        for (int i = 0; i < plan.items && block_merge; ++i) {
+            const int a = plan.item_seg_begin[i], z = plan.item_seg_begin[i + 1];
+            if (z - a <= 1) continue;
+            if (unit_of[static_cast<size_t>(a)] / pa::kBlockUnits != unit_of[static_cast<size_t>(z - 1)] / pa::kBlockUnits)
+                block_merge = false;   // the row spans blocks
+            for (int sg = a; sg < z && block_merge; ++sg) {
+                const int u = unit_of[static_cast<size_t>(sg)];
+                if (sg != plan.cta_seg_begin[u] && sg != plan.cta_seg_begin[u + 1] - 1)
+                    block_merge = false;   // a split segment inside a unit
+            }
+        }
+    }
+    dp.block_merge = block_merge;
+    dp.needs_merge = !block_merge && nseg > static_cast<size_t>(plan.items) ? 1 : 0;
     dp.max_item_segments = 0;
     for (int i = 0; i < plan.items; ++i)
         dp.max_item_segments = std::max(dp.max_item_segments, plan.item_seg_begin[i + 1] - plan.item_seg_begin[i]);
@@ -235,6 +259,7 @@ void device_plan_bind(const pa_device_plan& dp, pa_decode_params& p) {
     p.partial_out    = dp.partial_out;
     p.partial_lse    = dp.partial_lse;
     p.max_item_segments = dp.max_item_segments;
+    p.block_merge       = dp.block_merge ? 1 : 0;
 }
 
 void device_plan_free(pa_device_plan& dp) {

@@ -36,6 +36,12 @@
 //   * Q of each segment is fetched compactly (G x 256 B across the wave) with
 //     the segment's first K/V loads and expanded to the B-operand layout
 //     through a per-wave LDS slot once per segment.
+//   * When every split row lies inside one block of 8 work units (as at
+//     C2 / C3 shapes) the rows are merged in the block and no merge launch is
+//     needed: a unit's split segments are only its first and last, so each
+//     wave records at most two in LDS; after one barrier the wave that holds a
+//     row's first split segment combines the row's partials (written by waves
+//     of the same CU, so visible after the workgroup barrier) into the output.
 
 #include "pa_device.hpp"
 
@@ -89,7 +95,7 @@
 namespace pa {
 namespace {
 
-constexpr int   kWaves        = 4;      // waves (work units) per 256-thread block
+constexpr int   kWaves        = kBlockUnits;   // waves (work units) per block
 constexpr float kRescaleSlack = 8.0f;   // log2 headroom of the lazy running max
 constexpr float kLog2e        = 1.4426950408889634f;
 // dword 3 of a raw buffer resource (32-bit data format, no swizzle), and the
@@ -162,6 +168,76 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, 
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, kBufferFlags);
 }
 
+// Block-level merge after the split loop. slot_item / slot_seg hold, per wave,
+// the (row, kv head) item and segment index of its first (slot 0) and last
+// (slot 1) segment when that segment is a split one, else item -1. Items appear
+// in block order (wave, slot) as contiguous runs (ignoring empty slots); the
+// wave holding a run's first slot merges the run: the base-2 LSE-weighted
+// average of the run's normalized partials (decode_kernels.cuh:409-432),
+// written as the fp16 output when the run is the whole row.
+template <int G>
+__device__ __forceinline__ void block_merge(const pa_decode_params& p, const int (*slot_item)[2],
+                                            const int (*slot_seg)[2], int wave, int lane) {
+    constexpr int NS = 2 * kWaves;
+    for (int sl = 0; sl < 2; ++sl) {
+        const int x = slot_item[wave][sl];
+        if (x < 0) continue;
+        int prev = -1;
+        for (int i = 2 * wave + sl - 1; i >= 0; --i)
+            if (slot_item[i >> 1][i & 1] >= 0) {
+                prev = slot_item[i >> 1][i & 1];
+                break;
+            }
+        if (prev == x) continue;   // another wave merges this run
+        int k = 0;
+        for (int i = 2 * wave + sl; i < NS; ++i) {
+            const int it = slot_item[i >> 1][i & 1];
+            if (it < 0) continue;
+            if (it != x) break;
+            ++k;
+        }
+        if (k != p.item_seg_begin[x + 1] - p.item_seg_begin[x]) continue;   // row spans blocks: merge kernel
+        const int b = x / p.num_kv_heads, h = x - b * p.num_kv_heads;
+#pragma unroll
+        for (int t = lane; t < 16 * G; t += 64) {
+            const int g  = t >> 4;
+            const int ch = t & 15;
+            float mx = -INFINITY;
+            for (int i = 2 * wave + sl, j = 0; j < k; ++i) {
+                if (slot_item[i >> 1][i & 1] < 0) continue;
+                mx = fmaxf(mx, p.partial_lse[static_cast<size_t>(slot_seg[i >> 1][i & 1]) * G + g]);
+                ++j;
+            }
+            f32x4 a0 = {0.f, 0.f, 0.f, 0.f}, a1 = {0.f, 0.f, 0.f, 0.f};
+            float den = 0.f;
+            for (int i = 2 * wave + sl, j = 0; j < k; ++i) {
+                if (slot_item[i >> 1][i & 1] < 0) continue;
+                const size_t sg = static_cast<size_t>(slot_seg[i >> 1][i & 1]);
+                const float  w  = exp2_fast(p.partial_lse[sg * G + g] - mx);
+                const f32x4* o  = reinterpret_cast<const f32x4*>(p.partial_out + (sg * G + g) * kHeadDim + 8 * ch);
+                const f32x4  lo = o[0], hi = o[1];
+#pragma unroll
+                for (int jj = 0; jj < 4; ++jj) {
+                    a0[jj] = fmaf(w, lo[jj], a0[jj]);
+                    a1[jj] = fmaf(w, hi[jj], a1[jj]);
+                }
+                den += w;
+                ++j;
+            }
+            const float inv = 1.0f / den;
+            u32x4 o;
+#pragma unroll
+            for (int jj = 0; jj < 2; ++jj) {
+                const f16x2 x0 = {static_cast<_Float16>(a0[2 * jj] * inv), static_cast<_Float16>(a0[2 * jj + 1] * inv)};
+                const f16x2 x1 = {static_cast<_Float16>(a1[2 * jj] * inv), static_cast<_Float16>(a1[2 * jj + 1] * inv)};
+                o[jj]     = __builtin_bit_cast(uint32_t, x0);
+                o[2 + jj] = __builtin_bit_cast(uint32_t, x1);
+            }
+            *reinterpret_cast<u32x4*>(p.out + (static_cast<size_t>(b) * p.num_q_heads + h * G + g) * kHeadDim + 8 * ch) = o;
+        }
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Split kernel body.
 //   EB    cache element bytes (2 fp16, 1 fp8)
@@ -187,14 +263,22 @@ __device__ __forceinline__ void decode_split_body(const pa_decode_params& p, int
     using KRaw = std::conditional_t<KL == 16, u32x4, u32x2>;
 
     __shared__ __attribute__((aligned(16))) u32x4 q_lds[kWaves][16 * G];   // G heads x 256 B per wave
+    __shared__ int slot_item[kWaves][2], slot_seg[kWaves][2];                // split segments per wave
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int unit = blockIdx.x * kWaves + wave;
-    if (unit >= p.num_ctas) return;
-    const int seg_begin = p.cta_seg_begin[unit];
-    const int seg_end   = p.cta_seg_begin[unit + 1];
-    if (seg_begin >= seg_end) return;
+    const bool merge_here = p.block_merge != 0;   // block-level merge of split rows
+    if (lane == 0) {
+        slot_item[wave][0] = -1;
+        slot_item[wave][1] = -1;
+    }
+    int seg_begin = 0, seg_end = 0;
+    if (unit < p.num_ctas) {
+        seg_begin = p.cta_seg_begin[unit];
+        seg_end   = p.cta_seg_begin[unit + 1];
+    }
+    if (seg_begin < seg_end) {
 
     const int c  = lane & 15;   // MFMA column / row index within a 16-block
     const int kb = lane >> 4;   // MFMA k-block
@@ -388,6 +472,11 @@ __device__ __forceinline__ void decode_split_body(const pa_decode_params& p, int
                 }
             }
         }
+        if (!whole && merge_here && lane == 0) {
+            const int sl = C.seg == seg_begin ? 0 : 1;   // a unit's split segments are its first and last
+            slot_item[wave][sl] = C.b * hkv + C.h;
+            slot_seg[wave][sl]  = C.seg;
+        }
         m_run = -INFINITY;
         l_run = 0.f;
 #pragma unroll
@@ -570,6 +659,12 @@ __device__ __forceinline__ void decode_split_body(const pa_decode_params& p, int
             lookup(s);
         }
     }
+    }   // seg_begin < seg_end
+
+    if (merge_here) {
+        __syncthreads();
+        block_merge<G>(p, slot_item, slot_seg, wave, lane);
+    }
 }
 
 // The kernels: one per element width, each with its own register budget.
@@ -597,9 +692,10 @@ __global__ __launch_bounds__(64 * WAVES) void decode_merge_kernel(const pa_decod
     const int b    = blockIdx.y;
     const int item = b * p.num_kv_heads + hqi / G;
     const int g    = hqi % G;
-    const int s0   = p.item_seg_begin[item];
-    const int n    = p.item_seg_begin[item + 1] - s0;
+    const int s0 = p.item_seg_begin[item];
+    const int n  = p.item_seg_begin[item + 1] - s0;
     if (n <= 1) return;
+    auto seg_of = [&](int i) -> size_t { return static_cast<size_t>(s0 + i); };
 
     __shared__ float red[WAVES];
     __shared__ float2 acc_lds[WAVES][64];
@@ -608,10 +704,9 @@ __global__ __launch_bounds__(64 * WAVES) void decode_merge_kernel(const pa_decod
     const int t    = threadIdx.x;
     const int lane = t & 63;
     const int wave = t >> 6;
-    const float* lse = p.partial_lse + static_cast<size_t>(s0) * G + g;
 
     float mx = -INFINITY;
-    for (int i = t; i < n; i += NT) mx = fmaxf(mx, lse[static_cast<size_t>(i) * G]);
+    for (int i = t; i < n; i += NT) mx = fmaxf(mx, p.partial_lse[seg_of(i) * G + g]);
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
     if (lane == 0) red[wave] = mx;
@@ -621,11 +716,11 @@ __global__ __launch_bounds__(64 * WAVES) void decode_merge_kernel(const pa_decod
     for (int w = 1; w < WAVES; ++w) mx = fmaxf(mx, red[w]);
 
     float n0 = 0.f, n1 = 0.f, den = 0.f;
-    const float* po = p.partial_out + (static_cast<size_t>(s0) * G + g) * kHeadDim + 2 * lane;
 #pragma unroll 8
     for (int i = wave; i < n; i += WAVES) {
-        const float wgt = exp2_fast(lse[static_cast<size_t>(i) * G] - mx);
-        const float2 o  = *reinterpret_cast<const float2*>(po + static_cast<size_t>(i) * G * kHeadDim);
+        const size_t sg  = seg_of(i);
+        const float  wgt = exp2_fast(p.partial_lse[sg * G + g] - mx);
+        const float2 o   = *reinterpret_cast<const float2*>(p.partial_out + (sg * G + g) * kHeadDim + 2 * lane);
         n0 = fmaf(wgt, o.x, n0);
         n1 = fmaf(wgt, o.y, n1);
         den += wgt;
@@ -760,7 +855,7 @@ hipError_t launch_decode_split(int dtype, const pa_decode_params& p, hipStream_t
     if (!p.q || !p.out || !p.k_cache || !p.v_cache || !p.block_table || !p.segments || !p.cta_seg_begin ||
         !p.item_seg_begin)
         throw std::invalid_argument("decode: null pointer in params");
-    if (p.needs_merge && (!p.partial_out || !p.partial_lse))
+    if ((p.needs_merge || p.block_merge) && (!p.partial_out || !p.partial_lse))
         throw std::invalid_argument("decode: split rows need the partial workspace");
     return dtype == PA_KV_FP16 ? launch_split_e<2>(p, g, s) : launch_split_e<1>(p, g, s);
 }

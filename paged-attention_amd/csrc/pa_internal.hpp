@@ -25,6 +25,7 @@ inline void hip_check(hipError_t e, const char* what) {
 
 constexpr int kHeadDim     = 128;   // the only head_dim the path supports (decode.cu:31-38)
 constexpr int kGroupTokens = 16;    // tokens per MFMA step of the decode kernel
+constexpr int kBlockUnits  = 8;     // work units (waves) per block of the decode kernel
 
 inline void check_kv_dtype(int dtype) {
     if (dtype != PA_KV_FP16 && dtype != PA_KV_FP8_E4M3)

@@ -240,3 +240,43 @@ def test_decoder_ragged_config4_subset():
     lens = [int(x) for x in rng.integers(128, 16385, size=16)]
     err, _ = _decoder_case(len(lens), lens, False, threads=16)
     assert err < TOL, err
+
+
+@pytest.mark.parametrize("fp8", DTYPES, ids=IDS)
+def test_block_merge_and_merge_kernel_agree(fp8):
+    """A plan whose split rows each lie in one block of 8 work units (8 units
+    per row) is merged inside the split kernel; forcing the merge kernel on the
+    same plan must give the same answer, both against the oracle."""
+    import torch
+    lens = [2048] * 8
+    q, k, v, table, ks, vs = _paged_inputs(len(lens), lens, 32, 8, 16, fp8, seed=5)
+    dt = pa_amd.FP8_E4M3 if fp8 else pa_amd.FP16
+    tile = pa_amd.tile_tokens(dt, D, 4)
+    units = len(lens) * 8 * 8                      # 8 units per (row, kv head)
+    plan = pa_amd.make_plan(dt, lens, 32, 8, D, units)
+    assert plan.num_ctas == units and len(plan.segments) == units and 2048 // tile % 8 == 0
+    dplan = pa_amd.DevicePlan()
+    dplan.upload(plan, 4, D)
+    outs = []
+    for force_kernel in (False, True):
+        p = pa_amd.DecodeParams()
+        p.q, p.k_cache, p.v_cache, p.block_table = q.data_ptr(), k.data_ptr(), v.data_ptr(), table.data_ptr()
+        out = torch.empty_like(q)
+        p.out = out.data_ptr()
+        p.block_table_stride = table.size(1)
+        p.batch, p.num_q_heads, p.num_kv_heads, p.head_dim, p.page_size = len(lens), 32, 8, D, 16
+        p.sm_scale, p.k_scale, p.v_scale = pa_amd.sm_scale(D), ks, vs
+        dplan.bind(p)
+        assert p.block_merge == 1 and p.needs_merge == 0
+        if force_kernel:
+            p.block_merge, p.needs_merge = 0, 1
+        pa_amd.paged_decode(dt, p)
+        torch.cuda.synchronize()
+        outs.append(out.float().cpu().numpy())
+    kb = k.view(torch.uint8).cpu().numpy() if fp8 else k.view(torch.int16).cpu().numpy().view(np.uint16)
+    vb = v.view(torch.uint8).cpu().numpy() if fp8 else v.view(torch.int16).cpu().numpy().view(np.uint16)
+    ref = oracle.paged_decode(dt, q.view(torch.int16).cpu().numpy().view(np.uint16), kb, vb, table.cpu().numpy(),
+                              np.asarray(lens, np.int32), 32, 8, D, 16, ks, vs, threads=16)
+    for o in outs:
+        assert float(np.max(np.abs(o - ref))) < TOL
+    assert float(np.max(np.abs(outs[0] - outs[1]))) < 1e-3
