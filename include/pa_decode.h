@@ -197,6 +197,12 @@ int       pa_pool_admit(pa_pool* pool);
  * that is not admitted. *first_new / *num_new give the new table entries. */
 pa_status pa_pool_reserve(pa_pool* pool, int slot, int n, int* ok, int* first_new, int* num_new);
 /* paged_kv_cache.cu:138-146 release. */
+/* The bookkeeping of append_batch below, one call for many slots:
+ * pa_pool_reserve(slots[i], counts[i]) for i = 0..n-1 in order, but
+ * all-or-nothing (*ok = 0, nothing changed, when the whole batch does not fit;
+ * errors raised before anything changes). Grows the reference's per-call
+ * reserve (paged_kv_cache.cu:95-121) to a batch. */
+pa_status pa_pool_reserve_batch(pa_pool* pool, const int32_t* slots, const int32_t* counts, int n, int* ok);
 pa_status pa_pool_release(pa_pool* pool, int slot);
 /* paged_kv_cache.cu:148-151 shuffle_free_pages: std::shuffle(mt19937(seed)). */
 void      pa_pool_shuffle_free_pages(pa_pool* pool, unsigned seed);
@@ -237,6 +243,17 @@ int       pa_cache_admit(pa_cache* cache);
 /* paged_kv_cache.cu:95-136 append (synchronizes `stream`, as the reference). */
 pa_status pa_cache_append(pa_cache* cache, int slot, const uint16_t* d_k, const uint16_t* d_v,
                           int n, void* stream, int* appended);
+/* paged_kv_cache.cu:95-136 append, batched across sequences: appends counts[i]
+ * tokens to slots[i] for i = 0..n-1 (host arrays; a slot may repeat, its
+ * tokens then follow in order). d_k / d_v hold every token, concatenated in
+ * entry order: [sum(counts)][Hkv][D] fp16. Pages are reserved all-or-nothing
+ * (*appended = 0 and nothing changed when the pool lacks pages). The new
+ * block-table entries and lengths go over in one pinned host-to-device copy and
+ * one kernel writes them together with every token (copy or E4M3 quantize): two
+ * stream operations, no stream synchronization. The call returns once its host
+ * staging is queued; it waits only for the batch before the previous one. */
+pa_status pa_cache_append_batch(pa_cache* cache, const int32_t* slots, const int32_t* counts, int n,
+                                const uint16_t* d_k, const uint16_t* d_v, void* stream, int* appended);
 pa_status pa_cache_release(pa_cache* cache, int slot);
 void      pa_cache_shuffle_free_pages(pa_cache* cache, unsigned seed);
 /* paged_kv_cache.cu:157-171 params(): cache-side fields of DecodeParams. */

@@ -9,6 +9,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstddef>
+#include <stdexcept>
 #include <vector>
 
 namespace decode {
@@ -59,6 +60,18 @@ public:
         int done = 0;
         detail::check(pa_cache_append(h_, slot, reinterpret_cast<const uint16_t*>(d_k),
                                       reinterpret_cast<const uint16_t*>(d_v), n, stream, &done));
+        return done != 0;
+    }
+    // Appends counts[i] tokens to slots[i] for every i with one host-to-device
+    // copy and one kernel, without synchronizing the stream. d_k / d_v hold the
+    // tokens concatenated in entry order; pages are reserved all-or-nothing.
+    bool append_batch(const std::vector<int>& slots, const std::vector<int>& counts, const half* d_k, const half* d_v,
+                      hipStream_t stream = 0) {
+        if (slots.size() != counts.size()) throw std::invalid_argument("append_batch: slots and counts differ in size");
+        int done = 0;
+        detail::check(pa_cache_append_batch(h_, slots.data(), counts.data(), static_cast<int>(slots.size()),
+                                            reinterpret_cast<const uint16_t*>(d_k),
+                                            reinterpret_cast<const uint16_t*>(d_v), stream, &done));
         return done != 0;
     }
     // Returns a slot's pages to the free list.

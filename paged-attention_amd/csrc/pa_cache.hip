@@ -1,6 +1,8 @@
 // gfx950 kernels around the decode path:
 //
 //   append_kernel        fp16 copy / FP8 E4M3 quantize + page scatter (paged_kv_cache.cu:15-39)
+//   append_batch_kernel  the same for a whole decode step's appends across sequences, plus the
+//                        new block-table entries and lengths, in one launch
 //   gather_kernel        block-table resolution probe (the decode kernel's row address function)
 //   stream_read_kernel   streaming read: cache flush and plain-copy ceiling (bench_decode.cu:70-78)
 //   fill_bytes_kernel    streaming write of a byte value (bench_decode.cu:61-68's fill role; the
@@ -8,6 +10,7 @@
 
 #include "pa_device.hpp"
 
+#include <algorithm>
 #include <cmath>
 #include <cstdint>
 #include <stdexcept>
@@ -42,25 +45,11 @@ __device__ __forceinline__ float f16_bits_to_f32(uint32_t h16) {
     return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(h16)));
 }
 
-// One thread per (token, kv head, 8-dim chunk).
+// Stores one 8-dim chunk of fp16 K and V at byte offset dst of the pools:
+// a bit copy (fp16) or e4m3(float(x) * inv_scale) (FP8, paged_kv_cache.cu:15-22).
 template <int EB>
-__global__ __launch_bounds__(256) void append_kernel(const uint16_t* __restrict__ k,
-                                                     const uint16_t* __restrict__ v, void* k_cache,
-                                                     void* v_cache, const int32_t* __restrict__ bt_row,
-                                                     int start_pos, int n, int hkv, int page_size,
-                                                     float inv_k, float inv_v) {
-    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= n * hkv * (kHeadDim / 8)) return;
-    const int chunk = idx & 15;
-    const int th    = idx >> 4;
-    const int h     = th % hkv;
-    const int i     = th / hkv;
-    const int pos   = start_pos + i;
-    const int page  = bt_row[pos / page_size];
-    const size_t dst = kv_row_offset<EB>(page, h, pos % page_size, page_size, hkv) + 8 * EB * chunk;
-    const size_t src = (static_cast<size_t>(i) * hkv + h) * kHeadDim + 8 * chunk;
-    const u32x4 kin  = *reinterpret_cast<const u32x4*>(k + src);
-    const u32x4 vin  = *reinterpret_cast<const u32x4*>(v + src);
+__device__ __forceinline__ void store_chunk(const u32x4 kin, const u32x4 vin, void* k_cache, void* v_cache, size_t dst,
+                                            float inv_k, float inv_v) {
     unsigned char* kc = static_cast<unsigned char*>(k_cache) + dst;
     unsigned char* vc = static_cast<unsigned char*>(v_cache) + dst;
     if constexpr (EB == 2) {
@@ -78,6 +67,65 @@ __global__ __launch_bounds__(256) void append_kernel(const uint16_t* __restrict_
         *reinterpret_cast<u32x2*>(kc) = ko;
         *reinterpret_cast<u32x2*>(vc) = vo;
     }
+}
+
+// One thread per (token, kv head, 8-dim chunk); token i goes to position
+// start_pos + i of the sequence whose block-table row is bt_row.
+template <int EB>
+__global__ __launch_bounds__(256) void append_kernel(const uint16_t* __restrict__ k,
+                                                     const uint16_t* __restrict__ v, void* k_cache,
+                                                     void* v_cache, const int32_t* __restrict__ bt_row,
+                                                     int start_pos, int n, int hkv, int page_size,
+                                                     float inv_k, float inv_v) {
+    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= n * hkv * (kHeadDim / 8)) return;
+    const int chunk = idx & 15;
+    const int th    = idx >> 4;
+    const int h     = th % hkv;
+    const int i     = th / hkv;
+    const int pos   = start_pos + i;
+    const int page  = bt_row[pos / page_size];
+    const size_t dst = kv_row_offset<EB>(page, h, pos % page_size, page_size, hkv) + 8 * EB * chunk;
+    const size_t src = (static_cast<size_t>(i) * hkv + h) * kHeadDim + 8 * chunk;
+    store_chunk<EB>(*reinterpret_cast<const u32x4*>(k + src), *reinterpret_cast<const u32x4*>(v + src), k_cache,
+                    v_cache, dst, inv_k, inv_v);
+}
+
+// A whole batch of appends in one launch (layout of AppendBatch::meta in
+// pa_internal.hpp). Threads cover max(n_tok * hkv * 16, n_tab, n_len); each
+// writes its 8-dim chunk, table entry and length where it has one. A token
+// finds its entry by binary search over the entries' first-token offsets, then
+// its page in the entry's page list: table entries are read from the staging
+// copy, never from the block table this launch is writing.
+template <int EB>
+__global__ __launch_bounds__(256) void append_batch_kernel(const AppendBatch a) {
+    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+    const int32_t* tok_begin = a.meta;
+    const int32_t* old_len   = a.meta + a.n_ent;
+    const int32_t* pl_begin  = a.meta + 2 * a.n_ent;
+    const int32_t* pages     = a.meta + 3 * a.n_ent;
+    const int32_t* tab       = pages + a.n_pl;
+    const int32_t* lens      = tab + 2 * a.n_tab;
+    if (idx < a.n_tab) a.table[tab[2 * idx]] = tab[2 * idx + 1];
+    if (idx < a.n_len) a.seq_lens[lens[2 * idx]] = lens[2 * idx + 1];
+    if (idx >= a.n_tok * a.hkv * (kHeadDim / 8)) return;
+    const int chunk = idx & 15;
+    const int th    = idx >> 4;
+    const int h     = th % a.hkv;
+    const int t     = th / a.hkv;
+    int lo = 0, hi = a.n_ent;   // last entry with tok_begin <= t (zero-count entries share the next one's)
+    while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (tok_begin[mid] <= t) lo = mid;
+        else hi = mid;
+    }
+    const int first = old_len[lo];
+    const int pos   = first + (t - tok_begin[lo]);
+    const int page  = pages[pl_begin[lo] + pos / a.page_size - first / a.page_size];
+    const size_t dst = kv_row_offset<EB>(page, h, pos % a.page_size, a.page_size, a.hkv) + 8 * EB * chunk;
+    const size_t src = (static_cast<size_t>(t) * a.hkv + h) * kHeadDim + 8 * chunk;
+    store_chunk<EB>(*reinterpret_cast<const u32x4*>(a.k + src), *reinterpret_cast<const u32x4*>(a.v + src),
+                    a.k_cache, a.v_cache, dst, a.inv_k, a.inv_v);
 }
 
 // One thread per (token, 8-dim chunk) of one kv head: raw cache bytes out,
@@ -142,6 +190,18 @@ hipError_t launch_append(int dtype, const uint16_t* k, const uint16_t* v, void* 
     else
         hipLaunchKernelGGL(append_kernel<1>, dim3(blocks), dim3(256), 0, s, k, v, k_cache, v_cache, bt_row,
                            start_pos, n, hkv, page_size, inv_k, inv_v);
+    return hipGetLastError();
+}
+
+hipError_t launch_append_batch(int dtype, const AppendBatch& a, hipStream_t s) {
+    check_kv_dtype(dtype);
+    const long threads = std::max<long>(static_cast<long>(a.n_tok) * a.hkv * (kHeadDim / 8), std::max(a.n_tab, a.n_len));
+    if (threads <= 0) return hipSuccess;
+    const int blocks = static_cast<int>((threads + 255) / 256);
+    if (dtype == PA_KV_FP16)
+        hipLaunchKernelGGL(append_batch_kernel<2>, dim3(blocks), dim3(256), 0, s, a);
+    else
+        hipLaunchKernelGGL(append_batch_kernel<1>, dim3(blocks), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 

@@ -54,6 +54,15 @@ struct pa_pool {
     std::vector<char>                 occupied;
 };
 
+// One host-to-device staging buffer of the batched append: pinned host ints,
+// their device copy, and an event recorded after the kernel that reads them.
+struct pa_stage {
+    int32_t*   host = nullptr;
+    int32_t*   dev  = nullptr;
+    size_t     cap  = 0;   // int32 elements
+    hipEvent_t done = nullptr;
+};
+
 struct pa_cache {
     pa_cache_config cfg{};
     pa_pool         pool;
@@ -67,6 +76,8 @@ struct pa_cache {
     pa_device_plan  dplan;
     int             plan_batch = 0;
     int             plan_hq    = 0;
+    pa_stage        stage[2];   // used in turn, so one batch may still be in flight while the next is staged
+    int             stage_next = 0;
 };
 
 namespace {
@@ -322,6 +333,50 @@ bool pool_reserve(pa_pool& pool, int slot, int n, int& first_new, int& num_new) 
     }
     pool.seq_lens[static_cast<size_t>(slot)] = static_cast<int32_t>(new_len);
     num_new = static_cast<int>(grow);
+    return true;
+}
+
+// Entry i of a batched append: the slot's length before it, and the table
+// entries it added.
+struct reserve_entry {
+    int old_len   = 0;
+    int first_new = 0;
+    int num_new   = 0;
+};
+
+// Batched append bookkeeping: the same as pool_reserve(slots[i], counts[i])
+// for i = 0..n-1 in order (a slot may repeat), except all-or-nothing: returns
+// false with nothing changed when the pool lacks pages for the whole batch, and
+// throws before changing anything for a bad slot, a negative count or a slot
+// that would exceed max_pages_per_slot.
+bool pool_reserve_batch(pa_pool& pool, const int32_t* slots, const int32_t* counts, int n,
+                        std::vector<reserve_entry>* entries) {
+    if (n < 0) throw std::invalid_argument("append_batch: negative batch size");
+    if (n > 0 && (!slots || !counts)) throw std::invalid_argument("append_batch: slots or counts is null");
+    std::vector<long> len(pool.seq_lens.begin(), pool.seq_lens.end());
+    std::vector<long> pages(static_cast<size_t>(pool.max_slots));
+    for (int s = 0; s < pool.max_slots; ++s) pages[static_cast<size_t>(s)] = static_cast<long>(pool.tables[static_cast<size_t>(s)].size());
+    long grow = 0;
+    for (int i = 0; i < n; ++i) {
+        if (!slot_ok(pool, slots[i])) throw std::invalid_argument("append_batch: slot is not admitted");
+        if (counts[i] < 0) throw std::invalid_argument("append_batch: negative token count");
+        const size_t s = static_cast<size_t>(slots[i]);
+        len[s] += counts[i];
+        const long need = (len[s] + pool.page_size - 1) / pool.page_size;
+        if (need > pool.max_pages_per_slot) throw std::length_error("append_batch: sequence exceeds max_pages_per_slot");
+        if (need > pages[s]) {
+            grow += need - pages[s];
+            pages[s] = need;
+        }
+    }
+    if (grow > static_cast<long>(pool.free_pages.size())) return false;
+    if (entries) entries->assign(static_cast<size_t>(n), reserve_entry{});
+    for (int i = 0; i < n; ++i) {
+        reserve_entry e;
+        e.old_len = pool.seq_lens[static_cast<size_t>(slots[i])];
+        pool_reserve(pool, slots[i], counts[i], e.first_new, e.num_new);
+        if (entries) (*entries)[static_cast<size_t>(i)] = e;
+    }
     return true;
 }
 
@@ -630,6 +685,14 @@ pa_status pa_pool_reserve(pa_pool* pool, int slot, int n, int* ok, int* first_ne
     });
 }
 
+pa_status pa_pool_reserve_batch(pa_pool* pool, const int32_t* slots, const int32_t* counts, int n, int* ok) {
+    return guarded([&] {
+        if (!pool) throw std::invalid_argument("pool is null");
+        const bool r = pool_reserve_batch(*pool, slots, counts, n, nullptr);
+        if (ok) *ok = r ? 1 : 0;
+    });
+}
+
 pa_status pa_pool_release(pa_pool* pool, int slot) {
     return guarded([&] {
         if (!pool) throw std::invalid_argument("pool is null");
@@ -720,6 +783,12 @@ void pa_cache_destroy(pa_cache* c) {
     (void)hipFree(c->d_table);
     (void)hipFree(c->d_seq_lens);
     (void)hipFree(c->d_slot_ids);
+    for (pa_stage& st : c->stage) {
+        if (st.done) (void)hipEventSynchronize(st.done);
+        (void)hipHostFree(st.host);
+        (void)hipFree(st.dev);
+        if (st.done) (void)hipEventDestroy(st.done);
+    }
     device_plan_free(c->dplan);
     delete c;
 }
@@ -758,10 +827,125 @@ pa_status pa_cache_append(pa_cache* c, int slot, const uint16_t* d_k, const uint
     });
 }
 
+namespace {
+
+// Takes the next staging buffer with room for `need` ints, waiting for the
+// batch that last used it (its copy and kernel) to finish.
+pa_stage& take_stage(pa_cache& c, size_t need) {
+    pa_stage& st = c.stage[c.stage_next];
+    c.stage_next ^= 1;
+    if (!st.done) pa::hip_check(hipEventCreateWithFlags(&st.done, hipEventDisableTiming), "hipEventCreate");
+    pa::hip_check(hipEventSynchronize(st.done), "hipEventSynchronize staging");
+    if (st.cap < need) {
+        const size_t cap = std::max<size_t>(need + need / 2, 4096);
+        (void)hipHostFree(st.host);
+        (void)hipFree(st.dev);
+        st.host = nullptr;
+        st.dev  = nullptr;
+        st.cap  = 0;
+        pa::hip_check(hipHostMalloc(reinterpret_cast<void**>(&st.host), cap * sizeof(int32_t), hipHostMallocDefault),
+                      "hipHostMalloc staging");
+        pa::hip_check(hipMalloc(reinterpret_cast<void**>(&st.dev), cap * sizeof(int32_t)), "hipMalloc staging");
+        st.cap = cap;
+    }
+    return st;
+}
+
+}  // namespace
+
+pa_status pa_cache_append_batch(pa_cache* c, const int32_t* slots, const int32_t* counts, int n, const uint16_t* d_k,
+                                const uint16_t* d_v, void* stream, int* appended) {
+    return guarded([&] {
+        if (!c) throw std::invalid_argument("cache is null");
+        if (appended) *appended = 0;
+        long n_tok = 0;
+        for (int i = 0; i < n && counts; ++i) n_tok += counts[i] > 0 ? counts[i] : 0;
+        const int hkv = c->cfg.num_kv_heads;
+        if (n_tok * hkv * (pa::kHeadDim / 8) > INT_MAX) throw std::length_error("append_batch: too many tokens");
+        if (n_tok > 0 && (!d_k || !d_v)) throw std::invalid_argument("append_batch: k or v is null");
+        std::vector<reserve_entry> entries;
+        if (!pool_reserve_batch(c->pool, slots, counts, n, &entries)) return;   // out of pages: nothing appended
+        if (appended) *appended = 1;
+        if (n_tok == 0) return;
+
+        // Staging (layout of pa::AppendBatch::meta): per entry its first
+        // token, old length and page-list start; the page lists; the new table
+        // entries; one (slot, length) per distinct slot.
+        const int P = c->cfg.page_size;
+        long n_tab = 0, n_pl = 0;
+        for (int i = 0; i < n; ++i) {
+            const reserve_entry& e = entries[static_cast<size_t>(i)];
+            n_tab += e.num_new;
+            if (counts[i] > 0) n_pl += (e.old_len + counts[i] - 1) / P - e.old_len / P + 1;
+        }
+        std::vector<char> seen(static_cast<size_t>(c->cfg.max_slots), 0);
+        long n_len = 0;
+        for (int i = 0; i < n; ++i)
+            if (!seen[static_cast<size_t>(slots[i])]) seen[static_cast<size_t>(slots[i])] = 1, ++n_len;
+        const size_t need = 3 * static_cast<size_t>(n) + static_cast<size_t>(n_pl) + 2 * static_cast<size_t>(n_tab + n_len);
+        pa_stage& st = take_stage(*c, need);
+        int32_t* tok_begin = st.host;
+        int32_t* old_len   = tok_begin + n;
+        int32_t* pl_begin  = old_len + n;
+        int32_t* pages     = pl_begin + n;
+        int32_t* tab       = pages + n_pl;
+        int32_t* lens      = tab + 2 * n_tab;
+        int32_t  tok = 0, pl = 0;
+        for (int i = 0; i < n; ++i) {
+            const auto& table = c->pool.tables[static_cast<size_t>(slots[i])];
+            const reserve_entry& e = entries[static_cast<size_t>(i)];
+            tok_begin[i] = tok;
+            old_len[i]   = e.old_len;
+            pl_begin[i]  = pl;
+            tok += counts[i];
+            if (counts[i] > 0)
+                for (int k = e.old_len / P; k <= (e.old_len + counts[i] - 1) / P; ++k) pages[pl++] = table[static_cast<size_t>(k)];
+            for (int k = e.first_new; k < e.first_new + e.num_new; ++k) {
+                *tab++ = slots[i] * c->cfg.max_pages_per_slot + k;
+                *tab++ = table[static_cast<size_t>(k)];
+            }
+        }
+        for (int i = 0; i < n; ++i) {
+            const size_t sl = static_cast<size_t>(slots[i]);
+            if (seen[sl] != 1) continue;
+            seen[sl] = 2;
+            *lens++ = slots[i];
+            *lens++ = c->pool.seq_lens[sl];
+        }
+
+        const hipStream_t s = as_stream(stream);
+        pa::hip_check(hipMemcpyAsync(st.dev, st.host, need * sizeof(int32_t), hipMemcpyHostToDevice, s),
+                      "hipMemcpyAsync append staging");
+        const bool fp8 = c->cfg.dtype == PA_KV_FP8_E4M3;
+        pa::AppendBatch a{};
+        a.k = d_k;
+        a.v = d_v;
+        a.k_cache = c->d_k;
+        a.v_cache = c->d_v;
+        a.meta = st.dev;
+        a.table = c->d_table;
+        a.seq_lens = c->d_seq_lens;
+        a.n_ent = n;
+        a.n_pl = static_cast<int>(n_pl);
+        a.n_tab = static_cast<int>(n_tab);
+        a.n_len = static_cast<int>(n_len);
+        a.n_tok = static_cast<int>(n_tok);
+        a.hkv = hkv;
+        a.page_size = P;
+        a.inv_k = fp8 ? 1.0f / c->cfg.k_scale : 1.0f;
+        a.inv_v = fp8 ? 1.0f / c->cfg.v_scale : 1.0f;
+        pa::hip_check(pa::launch_append_batch(c->cfg.dtype, a, s), "append_batch kernel launch");
+        pa::hip_check(hipEventRecord(st.done, s), "hipEventRecord staging");
+    });
+}
+
 pa_status pa_cache_release(pa_cache* c, int slot) {
     return guarded([&] {
         if (!c) throw std::invalid_argument("cache is null");
         pool_release(c->pool, slot);
+        // A batched append still in flight may write this slot's length.
+        for (pa_stage& st : c->stage)
+            if (st.done) pa::hip_check(hipEventSynchronize(st.done), "hipEventSynchronize staging");
         pa::hip_check(hipMemset(c->d_seq_lens + slot, 0, sizeof(int32_t)), "hipMemset seq_len");
     });
 }

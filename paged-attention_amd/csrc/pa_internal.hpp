@@ -45,6 +45,26 @@ hipError_t launch_decode_merge(int dtype, const pa_decode_params& p, hipStream_t
 hipError_t launch_append(int dtype, const uint16_t* k, const uint16_t* v, void* k_cache,
                          void* v_cache, const int32_t* bt_row, int start_pos, int n, int hkv,
                          int page_size, float inv_k, float inv_v, hipStream_t s);
+// One launch of the batched append. meta (int32, device), for n_ent entries:
+//   tok_begin[n_ent]  first token of each entry in k / v (prefix sums of the counts)
+//   old_len[n_ent]    the slot's length before the entry
+//   pl_begin[n_ent]   the entry's first page in pages[]
+//   pages[n_pl]       per entry, the pages holding positions old_len .. old_len + count - 1
+//   tab[2 n_tab]      new block-table entries: flat index, page
+//   lens[2 n_len]     new lengths, one per distinct slot: slot, length
+struct AppendBatch {
+    const uint16_t* k;
+    const uint16_t* v;
+    void*           k_cache;
+    void*           v_cache;
+    const int32_t*  meta;
+    int32_t*        table;
+    int32_t*        seq_lens;
+    int             n_ent, n_pl, n_tab, n_len, n_tok;
+    int             hkv, page_size;
+    float           inv_k, inv_v;
+};
+hipError_t launch_append_batch(int dtype, const AppendBatch& a, hipStream_t s);
 hipError_t launch_gather(int dtype, const void* cache, const int32_t* bt_row, int hkv,
                          int page_size, int kv_head, int len, void* out, hipStream_t s);
 hipError_t launch_fill_bytes(void* buf, size_t bytes, int value, hipStream_t s);

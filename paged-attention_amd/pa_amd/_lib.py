@@ -133,6 +133,7 @@ SIGNATURES: dict[str, tuple] = {
     "pa_pool_destroy": (None, [_P]),
     "pa_pool_admit": (_I, [_P]),
     "pa_pool_reserve": (_I, [_P, _I, _I, _PI, _PI, _PI]),
+    "pa_pool_reserve_batch": (_I, [_P, _P, _P, _I, _PI]),
     "pa_pool_release": (_I, [_P, _I]),
     "pa_pool_shuffle_free_pages": (None, [_P, _U]),
     "pa_pool_free_pages": (_I, [_P]),
@@ -148,6 +149,7 @@ SIGNATURES: dict[str, tuple] = {
     "pa_cache_pool": (_P, [_P]),
     "pa_cache_admit": (_I, [_P]),
     "pa_cache_append": (_I, [_P, _I, _P, _P, _I, _P, _PI]),
+    "pa_cache_append_batch": (_I, [_P, _P, _P, _I, _P, _P, _P, _PI]),
     "pa_cache_release": (_I, [_P, _I]),
     "pa_cache_shuffle_free_pages": (None, [_P, _U]),
     "pa_cache_params": (_I, [_P, ctypes.POINTER(DecodeParams)]),

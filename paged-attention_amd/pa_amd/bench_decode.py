@@ -7,6 +7,7 @@ flags and columns as the reference's bench/bench_decode.cu:1-16:
     python -m pa_amd.bench_decode capacity  [--budget-gib G]     sequences per KV budget
     python -m pa_amd.bench_decode copy                           attainable read bandwidth
     python -m pa_amd.bench_decode single    --batch B --len L    one configuration
+    python -m pa_amd.bench_decode append    --batch B --len L    per-slot vs batched append
 
 Common flags: --hq 32 --hkv 8 --dim 128 --page 16 --iters 50 --dtype fp16|fp8
               --ctas N (0 = default grid) --contiguous-pages (no free-list shuffle)
@@ -195,6 +196,67 @@ SWEEP_SHAPES = [(1, 4096), (1, 16384), (1, 65536), (1, 131072), (8, 4096), (8, 1
                 (32, 1024), (32, 4096), (32, 8192), (64, 1024), (64, 4096), (128, 1024), (128, 2048)]
 
 
+def append_rows(batch: int, hkv: int, dim: int, page: int, fp8: bool, steps: int, prefill: int) -> list[dict]:
+    """Cost of growing the cache (paged_kv_cache.cu:95-136). A decode step
+    appends one token to each of `batch` sequences: `batch` append calls (each
+    synchronizes its stream, as the reference's) against one append_batch call
+    (one pinned copy + one kernel, no synchronization); wall time per step over
+    `steps` steps. Then a prefill of `prefill` tokens per sequence through one
+    append_batch call, timed with events (host staging and its copy included;
+    median of 5); bytes = fp16 K and V read + K and V written at the cache's
+    width."""
+    import time
+
+    import torch
+    dt = core.FP8_E4M3 if fp8 else core.FP16
+    eb = 1 if fp8 else 2
+    per_seq = 2 * steps + 6 * prefill
+    max_pages = math.ceil(per_seq / page)
+    cache = core.PagedKVCache(batch * max_pages, page, hkv, dim, batch, max_pages, dt, 4.0 / 448, 4.0 / 448)
+    slots = [cache.admit() for _ in range(batch)]
+    ones = [1] * batch
+    k1 = torch.randn(batch, hkv, dim, device="cuda", dtype=torch.float16)
+    v1 = torch.randn_like(k1)
+    sh = torch.cuda.current_stream()
+    rows = []
+    row_bytes = hkv * dim * 2
+
+    def per_slot():
+        for b in slots:
+            cache.append(b, k1.data_ptr() + b * row_bytes, v1.data_ptr() + b * row_bytes, 1, sh)
+
+    def batched():
+        cache.append_batch(slots, ones, k1, v1, sh)
+
+    for name, fn in (("per_slot", per_slot), ("batched", batched)):
+        fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps - 1):
+            fn()
+        torch.cuda.synchronize()
+        us = (time.perf_counter() - t0) / (steps - 1) * 1e6
+        nbytes = batch * row_bytes * 2 + batch * hkv * dim * eb * 2
+        rows.append(dict(mode=name, tokens=1, calls=batch if name == "per_slot" else 1, us=us,
+                         gbps=nbytes / (us * 1e-6) / 1e9))
+    kp = torch.randn(batch * prefill, hkv, dim, device="cuda", dtype=torch.float16)
+    vp = torch.randn_like(kp)
+    counts = [prefill] * batch
+    ms = []
+    for _ in range(5):   # the first call of each of the two staging buffers allocates it
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        assert cache.append_batch(slots, counts, kp, vp, sh)
+        e1.record()
+        torch.cuda.synchronize()
+        ms.append(e0.elapsed_time(e1))
+    us = statistics.median(ms) * 1e3
+    nbytes = batch * prefill * (row_bytes * 2 + hkv * dim * eb * 2)
+    rows.append(dict(mode="prefill_batched", tokens=prefill, calls=1, us=us, gbps=nbytes / (us * 1e-6) / 1e9))
+    cache.close()
+    return rows
+
+
 def _parse(argv: list[str]):
     mode = "sweep"
     kv: dict[str, str] = {}
@@ -247,8 +309,16 @@ def main(argv: list[str] | None = None) -> int:
                   f"{100 * r['gbps'] / peak:.1f}", flush=True)
         return 0
 
-    fl = None if "warm" in a else Flusher()
     fp8 = a.get("dtype", "fp16") == "fp8"
+    if mode == "append":
+        print("gpu,dtype,mode,batch,tokens_per_seq,calls_per_step,us_per_step,gbps,pct_peak")
+        b = geti("batch", 64)
+        for r in append_rows(b, hkv, dim, page, fp8, geti("steps", 200), geti("len", 1024)):
+            print(f"{gpu},{'fp8_e4m3' if fp8 else 'fp16'},{r['mode']},{b},{r['tokens']},{r['calls']},"
+                  f"{r['us']:.2f},{r['gbps']:.1f},{100 * r['gbps'] / peak:.1f}", flush=True)
+        return 0
+
+    fl = None if "warm" in a else Flusher()
     if mode == "sweep":
         print(HEADER)
         dts = [fp8] if "dtype" in a else [False, True]

@@ -224,6 +224,17 @@ class PagePool:
              ctypes.byref(num))
         return bool(ok.value), first.value, num.value
 
+    def reserve_batch(self, slots, counts) -> bool:
+        """reserve(slots[i], counts[i]) for every i in order, all-or-nothing."""
+        slots = np.ascontiguousarray(slots, dtype=np.int32)
+        counts = np.ascontiguousarray(counts, dtype=np.int32)
+        if slots.shape != counts.shape or slots.ndim != 1:
+            raise ValueError("slots and counts must be 1-D of one length")
+        ok = ctypes.c_int()
+        call("pa_pool_reserve_batch", self._h, slots.ctypes.data, counts.ctypes.data, slots.size,
+             ctypes.byref(ok))
+        return bool(ok.value)
+
     def release(self, slot: int) -> None:
         call("pa_pool_release", self._h, slot)
 
@@ -284,6 +295,19 @@ class PagedKVCache:
     def append(self, slot: int, k, v, n: int, stream=None) -> bool:
         done = ctypes.c_int(0)
         call("pa_cache_append", self._h, slot, _ptr(k), _ptr(v), n, _stream(stream), ctypes.byref(done))
+        return bool(done.value)
+
+    def append_batch(self, slots, counts, k, v, stream=None) -> bool:
+        """Appends counts[i] tokens to slots[i] for every i in one copy + one
+        kernel; k / v hold the tokens concatenated in entry order
+        ([sum(counts)][Hkv][D] fp16, device). All-or-nothing on pages."""
+        slots = np.ascontiguousarray(slots, dtype=np.int32)
+        counts = np.ascontiguousarray(counts, dtype=np.int32)
+        if slots.shape != counts.shape or slots.ndim != 1:
+            raise ValueError("slots and counts must be 1-D of one length")
+        done = ctypes.c_int(0)
+        call("pa_cache_append_batch", self._h, slots.ctypes.data, counts.ctypes.data, slots.size,
+             _ptr(k), _ptr(v), _stream(stream), ctypes.byref(done))
         return bool(done.value)
 
     def release(self, slot: int) -> None:

@@ -109,10 +109,11 @@ std::vector<T> to_host(const T* d, size_t n) {
 }
 
 // tests/test_paged_decode.cu:50-151 run_case through decode::PagedKVCache:
-// append (whole or round-robin chunks), decode, then compare with the oracle
-// over the stored cache contents. Returns the max-abs error.
+// append (whole or round-robin chunks; with `batched` every round of chunks is
+// one append_batch call), decode, then compare with the oracle over the stored
+// cache contents. Returns the max-abs error.
 double run_case(decode::KVDtype dtype, int hq, int hkv, int page, const std::vector<int>& lens, int chunk,
-                int ctas, bool shuffle) {
+                int ctas, bool shuffle, bool batched) {
     using namespace decode;
     std::mt19937 rng(1234);
     const int B = static_cast<int>(lens.size());
@@ -143,18 +144,41 @@ double run_case(decode::KVDtype dtype, int hq, int hkv, int page, const std::vec
         dV.push_back(to_device(V[static_cast<size_t>(b)]));
     }
     std::vector<int> done(static_cast<size_t>(B), 0);
+    const size_t row = static_cast<size_t>(hkv) * kD;
+    uint16_t *bk = nullptr, *bv = nullptr;   // one round's tokens, concatenated
+    size_t total = 0;
+    for (int L : lens) total += static_cast<size_t>(L);
+    if (batched) {
+        HIP_CHECK(hipMalloc(&bk, sizeof(uint16_t) * total * row));
+        HIP_CHECK(hipMalloc(&bv, sizeof(uint16_t) * total * row));
+    }
     for (bool more = true; more;) {
         more = false;
+        std::vector<int> slots, counts;
+        size_t at = 0;
         for (int b = 0; b < B; ++b) {
             const int n = std::min(chunk > 0 ? chunk : lens[b], lens[b] - done[b]);
             if (n <= 0) continue;
-            const size_t off = static_cast<size_t>(done[b]) * hkv * kD;
-            expect(cache.append(b, reinterpret_cast<const half*>(dK[b] + off),
-                                reinterpret_cast<const half*>(dV[b] + off), n),
-                   "append fits");
+            const size_t off = static_cast<size_t>(done[b]) * row;
+            if (batched) {
+                HIP_CHECK(hipMemcpy(bk + at * row, dK[b] + off, sizeof(uint16_t) * n * row, hipMemcpyDeviceToDevice));
+                HIP_CHECK(hipMemcpy(bv + at * row, dV[b] + off, sizeof(uint16_t) * n * row, hipMemcpyDeviceToDevice));
+                slots.push_back(b);
+                counts.push_back(n);
+                at += static_cast<size_t>(n);
+            } else {
+                expect(cache.append(b, reinterpret_cast<const half*>(dK[b] + off),
+                                    reinterpret_cast<const half*>(dV[b] + off), n),
+                       "append fits");
+            }
             done[b] += n;
             more = true;
         }
+        if (!slots.empty())
+            expect(cache.append_batch(slots, counts, reinterpret_cast<const half*>(bk),
+                                      reinterpret_cast<const half*>(bv)),
+                   "append_batch fits");
+        // The next round's copies overwrite bk / bv (null stream, which waits for the batch kernel).
     }
     for (int b = 0; b < B; ++b) expect(cache.seq_len(b) == lens[b], "seq_len after append");
     uint16_t* dq = to_device(q);
@@ -208,6 +232,8 @@ double run_case(decode::KVDtype dtype, int hq, int hkv, int page, const std::vec
     HIP_CHECK(hipFree(dq));
     HIP_CHECK(hipFree(dout));
     HIP_CHECK(hipFree(dout2));
+    if (bk) HIP_CHECK(hipFree(bk));
+    if (bv) HIP_CHECK(hipFree(bv));
     return err;
 }
 
@@ -219,6 +245,7 @@ void gpu_checks() {
         std::vector<int> lens;
         int chunk, ctas;
         bool shuffle;
+        bool batched = false;
     };
     const std::vector<Case> cases = {
         {KVDtype::FP16, 32, 8, 16, {1}, 0, 0, false},
@@ -230,10 +257,12 @@ void gpu_checks() {
         {KVDtype::FP16, 16, 4, 128, {300, 2500}, 0, 0, false},
         {KVDtype::FP8_E4M3, 32, 8, 16, {5000, 90, 1, 700}, 0, 7, false},
         {KVDtype::FP16, 32, 8, 16, {400, 333, 612}, 5, 0, true},
+        {KVDtype::FP8_E4M3, 32, 8, 16, {400, 333, 612}, 1, 0, true, true},
+        {KVDtype::FP16, 16, 4, 8, {40, 1, 95}, 3, 0, true, true},
     };
     for (size_t i = 0; i < cases.size(); ++i) {
         const Case& c = cases[i];
-        const double err = run_case(c.dt, c.hq, c.hkv, c.page, c.lens, c.chunk, c.ctas, c.shuffle);
+        const double err = run_case(c.dt, c.hq, c.hkv, c.page, c.lens, c.chunk, c.ctas, c.shuffle, c.batched);
         char buf[160];
         std::snprintf(buf, sizeof buf, "case %zu (%s, hq %d hkv %d page %d): max|gpu - oracle| = %.3g", i,
                       decode::kv_dtype_name(c.dt), c.hq, c.hkv, c.page, err);

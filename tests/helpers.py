@@ -59,13 +59,15 @@ def dtype_of(fp8: bool) -> int:
 
 def run_cache_case(fp8: bool, hq: int, hkv: int, page_size: int, seq_lens, num_ctas: int = 0,
                    chunk: int = 0, seed: int = 1234, quantized_reference: bool = True,
-                   shuffle_seed: int | None = None, threads: int = 8):
+                   shuffle_seed: int | None = None, threads: int = 8, batched: bool = False):
     """tests/test_paged_decode.cu:50-151 run_case through the C ABI's cache.
 
     Builds a PagedKVCache, appends per-sequence K/V (whole or round-robin
-    chunks), decodes, and checks (1) every stored byte against the oracle's
-    append (bit-exact block-table scatter and FP8 bytes) and (2) the output
-    against the oracle's fp32 attention over the stored (dequantized) values.
+    chunks; with batched=True each round of chunks is one append_batch call,
+    as a decode step grows every sequence at once), decodes, and checks (1)
+    every stored byte against the oracle's append (bit-exact block-table
+    scatter and FP8 bytes) and (2) the output against the oracle's fp32
+    attention over the stored (dequantized) values.
     Returns (max_abs_err, out fp32, plan).
     """
     import torch
@@ -89,14 +91,24 @@ def run_cache_case(fp8: bool, hq: int, hkv: int, page_size: int, seq_lens, num_c
     progress = True
     while progress:
         progress = False
+        slots, counts, kparts, vparts = [], [], [], []
         for b in range(B):
             n = min(chunk if chunk > 0 else seq_lens[b], seq_lens[b] - done[b])
             if n <= 0:
                 continue
-            ok = cache.append(b, dK[b].data_ptr() + done[b] * row * 2, dV[b].data_ptr() + done[b] * row * 2, n)
-            assert ok
+            if batched:
+                slots.append(b)
+                counts.append(n)
+                kparts.append(dK[b][done[b]:done[b] + n])
+                vparts.append(dV[b][done[b]:done[b] + n])
+            else:
+                ok = cache.append(b, dK[b].data_ptr() + done[b] * row * 2, dV[b].data_ptr() + done[b] * row * 2, n)
+                assert ok
             done[b] += n
             progress = True
+        if slots:
+            kb, vb = torch.cat(kparts).contiguous(), torch.cat(vparts).contiguous()
+            assert cache.append_batch(slots, counts, kb, vb, torch.cuda.current_stream().cuda_stream)
     dq = to_device(q)
     dout = torch.empty((B, hq, D), dtype=torch.float16, device="cuda")
     cache.decode(dq, dout, B, hq, num_ctas)

@@ -122,6 +122,81 @@ def test_append_fp8_bytes_exhaustive(scale):
 
 
 @pytest.mark.parametrize("fp8", DTYPES, ids=IDS)
+@pytest.mark.parametrize("page_size,chunk", [(16, 1), (16, 7), (5, 3), (64, 0)])
+def test_append_batch_decode_steps(fp8, page_size, chunk):
+    """Sequences grown by batched appends (chunk=1: one token per sequence per
+    call, as a decode step; many calls back to back, no synchronization between
+    them): stored bytes bit-exact and decode within TOL of the oracle."""
+    err, _, _ = run_cache_case(fp8, 32, 8, page_size, [1, 17, 100, 333, 16], chunk=chunk, shuffle_seed=11,
+                               batched=True)
+    assert err <= TOL
+
+
+def _device_state(cache, slots, max_pages):
+    p = cache.params()
+    table = d2h(p.block_table, 4 * len(slots) * max_pages, np.int32).reshape(len(slots), max_pages)
+    lens = d2h(p.seq_lens, 4 * len(slots), np.int32)
+    return table, lens
+
+
+@pytest.mark.parametrize("fp8", DTYPES, ids=IDS)
+def test_append_batch_matches_sequential_appends(fp8):
+    """Two caches, same shuffled free list: one grown by append (one call per
+    slot and chunk), the other by append_batch with the same entries (a slot
+    repeated within a batch, zero counts). Pools, device block tables and
+    device lengths are bit-identical; an all-or-nothing refusal changes none."""
+    import torch
+    dt = pa_amd.FP8_E4M3 if fp8 else pa_amd.FP16
+    hkv, P, slots_n, max_pages = 4, 8, 4, 12
+    rng = np.random.default_rng(5)
+    caches = [pa_amd.PagedKVCache(30, P, hkv, D, slots_n, max_pages, dt, 4.0 / 448, 3.0 / 448) for _ in range(2)]
+    for c in caches:
+        c.shuffle_free_pages(3)
+        for _ in range(slots_n):
+            c.admit()
+    rounds = [([0, 1, 2, 3], [1, 9, 0, 17]), ([2, 0, 2], [5, 8, 3]), ([3, 1, 0, 2], [1, 1, 1, 1]),
+              ([1], [30])]
+    for slots, counts in rounds:
+        total = sum(counts)
+        k = to_device(normal_f16(rng, (total, hkv, D)))
+        v = to_device(normal_f16(rng, (total, hkv, D)))
+        off = 0
+        for s_, n in zip(slots, counts):
+            assert caches[0].append(s_, k.data_ptr() + off * hkv * D * 2, v.data_ptr() + off * hkv * D * 2, n)
+            off += n
+        assert caches[1].append_batch(slots, counts, k, v)
+    # 18 pages are free; growing slots 0 and 2 to 90 and 89 tokens needs 10 + 10.
+    free = caches[1].pool.free_pages()
+    assert free == 18
+    big = to_device(normal_f16(rng, (160, hkv, D)))
+    assert not caches[1].append_batch([0, 2], [80, 80], big, big)
+    assert caches[1].pool.free_pages() == free
+    torch.cuda.synchronize()
+    eb = 1 if fp8 else 2
+    nbytes = 30 * hkv * P * D * eb
+    pa, pb = caches[0].params(), caches[1].params()
+    view = (lambda a: a) if fp8 else (lambda a: a.view(np.uint16))
+    pools = [[view(d2h(getattr(p_, f), nbytes)) for f in ("k_cache", "v_cache")] for p_ in (pa, pb)]
+    for s_ in range(slots_n):   # pools are not cleared at creation: compare the stored tokens
+        t = caches[0].block_table(s_)
+        assert list(t) == list(caches[1].block_table(s_))
+        for h in range(hkv):
+            for f in range(2):
+                a = oracle.gather_raw(dt, pools[0][f], t, hkv, D, P, h, caches[0].seq_len(s_))
+                b = oracle.gather_raw(dt, pools[1][f], t, hkv, D, P, h, caches[1].seq_len(s_))
+                assert np.array_equal(a, b), f"slot {s_} head {h} {'kv'[f]}"
+    ta, la = _device_state(caches[0], range(slots_n), max_pages)
+    tb, lb = _device_state(caches[1], range(slots_n), max_pages)
+    assert np.array_equal(ta, tb) and np.array_equal(la, lb)
+    assert list(lb) == [caches[1].seq_len(s_) for s_ in range(slots_n)] == [10, 40, 9, 18]
+    for s_ in range(slots_n):
+        t = caches[1].block_table(s_)
+        assert list(tb[s_, :len(t)]) == list(t)
+    for c in caches:
+        c.close()
+
+
+@pytest.mark.parametrize("fp8", DTYPES, ids=IDS)
 @pytest.mark.parametrize("page_size,start", [(1, 0), (3, 5), (16, 0), (16, 9), (64, 100)])
 def test_append_and_gather_bit_exact(fp8, page_size, start):
     """Append at an offset into scattered pages, then read it back through the

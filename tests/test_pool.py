@@ -113,3 +113,54 @@ def test_errors():
     with pytest.raises(pa_amd.InvalidArgument):
         pool.release(1)
     assert pool.admit() == 1 and pool.admit() == -1
+
+
+def _twin_pools(seed=7):
+    a, b = pa_amd.PagePool(40, 4, 6, 12), pa_amd.PagePool(40, 4, 6, 12)
+    for p in (a, b):
+        p.shuffle_free_pages(seed)
+        for _ in range(5):
+            p.admit()
+    return a, b
+
+
+def _state(pool, slots=range(5)):
+    return pool.free_pages(), [(pool.seq_len(s), list(pool.block_table(s))) for s in slots]
+
+
+def test_reserve_batch_equals_sequential_reserves():
+    """A batch (with a repeated slot and a zero count) hands out the same pages,
+    in the same order, as the reserves it stands for, made one by one."""
+    a, b = _twin_pools()
+    rounds = [([0, 1, 2, 3, 4], [3, 1, 9, 0, 4]), ([2, 0, 2, 4], [2, 5, 7, 1]), ([1, 3], [16, 4])]
+    for slots, counts in rounds:
+        assert a.reserve_batch(slots, counts)
+        for s, n in zip(slots, counts):
+            assert b.reserve(s, n)[0]
+        assert _state(a) == _state(b)
+    assert a.seq_len(2) == 18 and len(a.block_table(2)) == 5
+
+
+def test_reserve_batch_is_all_or_nothing():
+    pool = pa_amd.PagePool(5, 4, 3, 8)
+    s0, s1 = pool.admit(), pool.admit()
+    assert pool.reserve_batch([s0, s1], [4, 5])            # 1 + 2 pages
+    before = _state(pool, (s0, s1))
+    assert not pool.reserve_batch([s0, s1], [5, 8])         # needs 2 + 2 more, 2 left
+    assert _state(pool, (s0, s1)) == before
+    assert pool.reserve_batch([s0, s1], [4, 4])             # 1 + 1: exactly the 2 left
+    assert pool.free_pages() == 0
+
+
+def test_reserve_batch_errors_change_nothing():
+    pool = pa_amd.PagePool(20, 4, 3, 3)
+    s0, s1 = pool.admit(), pool.admit()
+    before = _state(pool, (s0, s1))
+    with pytest.raises(pa_amd.LengthError, match="max_pages_per_slot"):
+        pool.reserve_batch([s0, s1, s1], [4, 8, 5])           # s1 reaches 13 > 12 tokens on its 2nd entry
+    with pytest.raises(pa_amd.InvalidArgument, match="not admitted"):
+        pool.reserve_batch([s0, 2], [1, 1])
+    with pytest.raises(pa_amd.InvalidArgument, match="negative"):
+        pool.reserve_batch([s0, s1], [1, -1])
+    assert _state(pool, (s0, s1)) == before
+    assert pool.reserve_batch([], [])
