@@ -45,6 +45,54 @@ __device__ __forceinline__ float f16_bits_to_f32(uint32_t h16) {
     return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(h16)));
 }
 
+// Streaming (non-temporal) loads of the new tokens and stores into the pages:
+// both are touched once per append.
+#ifndef PA_APPEND_NT
+#define PA_APPEND_NT 1
+#endif
+constexpr bool kAppendNT = PA_APPEND_NT != 0;
+
+// E4M3 encode of eight products float(x) * inv through gfx950's OCP FP8
+// conversion (v_cvt_scalef32_pk_fp8_f32, scale 1): each product is rounded to
+// fp32 first, as e4m3_encode's argument is. Finite values are clamped to
+// +-448 beforehand (saturation, and infinities). The instruction writes every
+// NaN as 0xff; a chunk holding a NaN takes e4m3_encode instead, which keeps
+// the sign (0x7f | sign), as the software path and the oracle do.
+#ifndef PA_APPEND_HWCVT
+#define PA_APPEND_HWCVT 1
+#endif
+constexpr bool kAppendHwCvt = PA_APPEND_HWCVT != 0;
+
+typedef short v2i16 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float sat448(float x) { return __builtin_fminf(__builtin_fmaxf(x, -448.0f), 448.0f); }
+
+__device__ __forceinline__ u32x2 encode8_hw(const u32x4 in, float inv) {
+    float f[8];
+    bool  nan = false;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        f[e] = f16_bits_to_f32((in[e >> 1] >> (16 * (e & 1))) & 0xffffu) * inv;
+        nan |= f[e] != f[e];
+    }
+    u32x2 out = {0u, 0u};
+    if (__builtin_expect(nan, 0)) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) out[e >> 2] |= e4m3_encode(f[e]) << (8 * (e & 3));
+        return out;
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) f[e] = sat448(f[e]);
+#pragma unroll
+    for (int w = 0; w < 2; ++w) {
+        v2i16 r = {0, 0};
+        r = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(r, f[4 * w + 0], f[4 * w + 1], 1.0f, false);
+        r = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(r, f[4 * w + 2], f[4 * w + 3], 1.0f, true);
+        out[w] = __builtin_bit_cast(uint32_t, r);
+    }
+    return out;
+}
+
 // Stores one 8-dim chunk of fp16 K and V at byte offset dst of the pools:
 // a bit copy (fp16) or e4m3(float(x) * inv_scale) (FP8, paged_kv_cache.cu:15-22).
 template <int EB>
@@ -53,19 +101,34 @@ __device__ __forceinline__ void store_chunk(const u32x4 kin, const u32x4 vin, vo
     unsigned char* kc = static_cast<unsigned char*>(k_cache) + dst;
     unsigned char* vc = static_cast<unsigned char*>(v_cache) + dst;
     if constexpr (EB == 2) {
-        *reinterpret_cast<u32x4*>(kc) = kin;
-        *reinterpret_cast<u32x4*>(vc) = vin;
+        if constexpr (kAppendNT) {
+            __builtin_nontemporal_store(kin, reinterpret_cast<u32x4*>(kc));
+            __builtin_nontemporal_store(vin, reinterpret_cast<u32x4*>(vc));
+        } else {
+            *reinterpret_cast<u32x4*>(kc) = kin;
+            *reinterpret_cast<u32x4*>(vc) = vin;
+        }
     } else {
         u32x2 ko = {0u, 0u}, vo = {0u, 0u};
+        if constexpr (kAppendHwCvt) {
+            ko = encode8_hw(kin, inv_k);
+            vo = encode8_hw(vin, inv_v);
+        } else {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const uint32_t kh = (kin[e >> 1] >> (16 * (e & 1))) & 0xffffu;
-            const uint32_t vh = (vin[e >> 1] >> (16 * (e & 1))) & 0xffffu;
-            ko[e >> 2] |= e4m3_encode(f16_bits_to_f32(kh) * inv_k) << (8 * (e & 3));
-            vo[e >> 2] |= e4m3_encode(f16_bits_to_f32(vh) * inv_v) << (8 * (e & 3));
+            for (int e = 0; e < 8; ++e) {
+                const uint32_t kh = (kin[e >> 1] >> (16 * (e & 1))) & 0xffffu;
+                const uint32_t vh = (vin[e >> 1] >> (16 * (e & 1))) & 0xffffu;
+                ko[e >> 2] |= e4m3_encode(f16_bits_to_f32(kh) * inv_k) << (8 * (e & 3));
+                vo[e >> 2] |= e4m3_encode(f16_bits_to_f32(vh) * inv_v) << (8 * (e & 3));
+            }
         }
-        *reinterpret_cast<u32x2*>(kc) = ko;
-        *reinterpret_cast<u32x2*>(vc) = vo;
+        if constexpr (kAppendNT) {
+            __builtin_nontemporal_store(ko, reinterpret_cast<u32x2*>(kc));
+            __builtin_nontemporal_store(vo, reinterpret_cast<u32x2*>(vc));
+        } else {
+            *reinterpret_cast<u32x2*>(kc) = ko;
+            *reinterpret_cast<u32x2*>(vc) = vo;
+        }
     }
 }
 
@@ -87,8 +150,7 @@ __global__ __launch_bounds__(256) void append_kernel(const uint16_t* __restrict_
     const int page  = bt_row[pos / page_size];
     const size_t dst = kv_row_offset<EB>(page, h, pos % page_size, page_size, hkv) + 8 * EB * chunk;
     const size_t src = (static_cast<size_t>(i) * hkv + h) * kHeadDim + 8 * chunk;
-    store_chunk<EB>(*reinterpret_cast<const u32x4*>(k + src), *reinterpret_cast<const u32x4*>(v + src), k_cache,
-                    v_cache, dst, inv_k, inv_v);
+    store_chunk<EB>(load16<kAppendNT>(k + src), load16<kAppendNT>(v + src), k_cache, v_cache, dst, inv_k, inv_v);
 }
 
 // A whole batch of appends in one launch (layout of AppendBatch::meta in
@@ -124,8 +186,8 @@ __global__ __launch_bounds__(256) void append_batch_kernel(const AppendBatch a) 
     const int page  = pages[pl_begin[lo] + pos / a.page_size - first / a.page_size];
     const size_t dst = kv_row_offset<EB>(page, h, pos % a.page_size, a.page_size, a.hkv) + 8 * EB * chunk;
     const size_t src = (static_cast<size_t>(t) * a.hkv + h) * kHeadDim + 8 * chunk;
-    store_chunk<EB>(*reinterpret_cast<const u32x4*>(a.k + src), *reinterpret_cast<const u32x4*>(a.v + src),
-                    a.k_cache, a.v_cache, dst, a.inv_k, a.inv_v);
+    store_chunk<EB>(load16<kAppendNT>(a.k + src), load16<kAppendNT>(a.v + src), a.k_cache, a.v_cache, dst, a.inv_k,
+                    a.inv_v);
 }
 
 // One thread per (token, 8-dim chunk) of one kv head: raw cache bytes out,

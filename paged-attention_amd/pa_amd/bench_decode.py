@@ -253,6 +253,21 @@ def append_rows(batch: int, hkv: int, dim: int, page: int, fp8: bool, steps: int
     us = statistics.median(ms) * 1e3
     nbytes = batch * prefill * (row_bytes * 2 + hkv * dim * eb * 2)
     rows.append(dict(mode="prefill_batched", tokens=prefill, calls=1, us=us, gbps=nbytes / (us * 1e-6) / 1e9))
+    # Read+write ceiling for comparison: a device-to-device copy of the fp16
+    # K and V (the runtime's copy kernel), same read bytes, fp16 write bytes.
+    dst = torch.empty_like(kp)
+    ms = []
+    for _ in range(5):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        dst.copy_(kp)
+        dst.copy_(vp)
+        e1.record()
+        torch.cuda.synchronize()
+        ms.append(e0.elapsed_time(e1))
+    us = statistics.median(ms) * 1e3
+    nbytes = 4 * kp.numel() * kp.element_size()
+    rows.append(dict(mode="d2d_copy_ceiling", tokens=prefill, calls=2, us=us, gbps=nbytes / (us * 1e-6) / 1e9))
     cache.close()
     return rows
 

@@ -16,6 +16,10 @@ Fixtures (data only; nothing here is reference source):
                     torch.float8_e4m3fn (an implementation independent of ours).
   e4m3_encode.npz   x (float32) and torch's E4M3 code for x, |x| < 464 only,
                     where torch and saturating (satfinite) conversion agree.
+  accuracy_rows.csv (dtype, batch, seq_len, max_abs_diff_vs_ref, fp8_err_vs_fp16,
+                    fp8_rel_err_vs_fp16): the accuracy columns of
+                    results/h100_flashinfer.csv (the reference kernel against its
+                    fp32 torch reference and FP8 against fp16 on the same seed).
 """
 
 from __future__ import annotations
@@ -52,6 +56,21 @@ def planner_rows(ref: pathlib.Path) -> list[dict]:
     return rows
 
 
+def accuracy_rows(ref: pathlib.Path) -> list[dict]:
+    keep = ("dtype", "batch", "seq_len", "max_abs_diff_vs_ref", "fp8_err_vs_fp16", "fp8_rel_err_vs_fp16")
+    with open(ref / "results" / "h100_flashinfer.csv") as f:
+        return [{k: r[k] for k in keep} for r in csv.DictReader(f)]
+
+
+def write_accuracy_rows(ref: pathlib.Path) -> None:
+    rows = accuracy_rows(ref)
+    with open(HERE / "accuracy_rows.csv", "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=list(rows[0].keys()))
+        w.writeheader()
+        w.writerows(rows)
+    print(f"accuracy_rows.csv: {len(rows)} rows")
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--reference", default="/root/reference")
@@ -67,6 +86,7 @@ def main() -> None:
 
     (HERE / "capacity_rows.csv").write_text((ref / "results" / "h100_capacity.csv").read_text())
     print("capacity_rows.csv written")
+    write_accuracy_rows(ref)
 
     import torch
 
