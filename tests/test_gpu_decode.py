@@ -269,7 +269,9 @@ def _paged_inputs(batch, seq_lens, hq, hkv, page_size, fp8, seed):
     return q, kc, vc, table, k_scale, v_scale
 
 
-def _decoder_case(batch, seq_lens, fp8, page_size=16, hq=32, hkv=8, seed=0, threads=16):
+def _decoder_case(batch, seq_lens, fp8, page_size=16, hq=32, hkv=8, seed=0, threads=16, rows=None):
+    """Decodes the whole batch on the GPU; checks every row against the oracle,
+    or only `rows` (a sample, for batches whose full oracle would take minutes)."""
     import torch
     q, k, v, table, ks, vs = _paged_inputs(batch, seq_lens, hq, hkv, page_size, fp8, seed)
     dec = pa_amd.Decoder(hq, hkv, D, page_size, fp8)
@@ -280,10 +282,11 @@ def _decoder_case(batch, seq_lens, fp8, page_size=16, hq=32, hkv=8, seed=0, thre
     dt = pa_amd.FP8_E4M3 if fp8 else pa_amd.FP16
     kb = k.view(torch.uint8).cpu().numpy() if fp8 else k.view(torch.int16).cpu().numpy().view(np.uint16)
     vb = v.view(torch.uint8).cpu().numpy() if fp8 else v.view(torch.int16).cpu().numpy().view(np.uint16)
-    ref = oracle.paged_decode(dt, q.view(torch.int16).cpu().numpy().view(np.uint16), kb, vb,
-                              table.cpu().numpy(), np.asarray(seq_lens, np.int32), hq, hkv, D, page_size, ks, vs,
-                              threads=threads)
-    got = out.float().cpu().numpy()
+    sel = np.arange(batch) if rows is None else np.asarray(rows)
+    qb = q.view(torch.int16).cpu().numpy().view(np.uint16)[sel]
+    ref = oracle.paged_decode(dt, qb, kb, vb, table.cpu().numpy()[sel], np.asarray(seq_lens, np.int32)[sel], hq,
+                              hkv, D, page_size, ks, vs, threads=threads)
+    got = out.float().cpu().numpy()[sel]
     return float(np.max(np.abs(got - ref))), dec
 
 
@@ -307,6 +310,60 @@ def test_decoder_long_context_config5_fp8():
     err, dec = _decoder_case(1, [131072], True, threads=8)
     assert dec.num_segments > 8 * 64
     assert err < TOL, err
+
+
+def test_decoder_full_size_config3():
+    """BASELINE config 3 at full size: 64 x 8192, FP8 E4M3 (amax/448 scales,
+    quantized by the append kernel), 16-token scattered pages."""
+    err, _ = _decoder_case(64, [8192] * 64, True, threads=16)
+    assert err < TOL, err
+
+
+def test_decoder_full_size_config4_sampled_rows():
+    """BASELINE config 4 at full size (128 ragged rows, L ~ U[128, 16384],
+    seed 4) decoded in one batch; 12 rows spread over the batch (first, last,
+    longest, shortest, 8 seeded) checked against the oracle."""
+    rng = np.random.default_rng(4)
+    lens = [int(x) for x in rng.integers(128, 16385, size=128)]
+    pick = {0, 127, int(np.argmax(lens)), int(np.argmin(lens))}
+    pick |= set(int(x) for x in np.random.default_rng(9).choice(128, 8, replace=False))
+    err, dec = _decoder_case(128, lens, False, threads=16, rows=sorted(pick))
+    assert dec.num_segments >= 128 * 8
+    assert err < TOL, err
+
+
+def test_decoder_long_context_config5_fp16():
+    """BASELINE config 5 (1 x 131072), fp16 KV."""
+    err, dec = _decoder_case(1, [131072], False, threads=8)
+    assert dec.num_segments > 8 * 64
+    assert err < TOL, err
+
+
+def test_full_size_output_invariant_under_page_placement():
+    """At config 2's full size the output is bitwise the same for two
+    different page permutations (the plan and tile order do not depend on
+    placement), a size-independent check of block-table resolution."""
+    import torch
+    outs = []
+    for seed in (0, 1):
+        g = torch.Generator(device="cuda").manual_seed(123)
+        n = 32 * 512
+        k = torch.randn(n, 8, 16, D, device="cuda", dtype=torch.float16, generator=g)
+        v = torch.randn(n, 8, 16, D, device="cuda", dtype=torch.float16, generator=g)
+        q = torch.randn(32, 32, D, device="cuda", dtype=torch.float16, generator=g)
+        logical = torch.arange(n, device="cuda", dtype=torch.int32).view(32, 512)
+        perm = torch.randperm(n, device="cuda", generator=torch.Generator(device="cuda").manual_seed(seed))
+        perm = perm.to(torch.int32)
+        kp, vp = torch.empty_like(k), torch.empty_like(v)
+        kp[perm.long()] = k                      # logical page i lives at physical page perm[i]
+        vp[perm.long()] = v
+        table = perm[logical.reshape(-1).long()].view(32, 512).contiguous()
+        dec = pa_amd.Decoder(32, 8, D, 16, False)
+        lens = torch.full((32,), 8192, dtype=torch.int32)
+        dec.plan(lens, 0)
+        outs.append(dec.run(q, kp, vp, table, lens.cuda(), 1.0, 1.0).view(torch.int16).cpu().numpy())
+        del k, v, kp, vp
+    assert np.array_equal(outs[0], outs[1])
 
 
 def test_decoder_ragged_config4_subset():
