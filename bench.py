@@ -20,8 +20,9 @@ Fields of the JSON line:
                8 TB/s
   cold         the reference's method: a 1 GiB flush before each run, HIP
                events around decode + merge, median of --cold-iters
-  copy_ceiling best plain streaming read of 4 GiB (bench_decode.cu:224-240
-               and unrolled variants of it)
+  copy_ceiling best plain streaming read of 4 GiB (bench_decode.cu:224-240,
+               unrolled / non-temporal variants of it, and the chunked read
+               with one contiguous span per wave)
   cpu_baseline the reference's cpu_attention (compiled from its source into
                oracle/_ref when that exists, else the oracle's restatement)
                over every (row, query head) pair of the same workload, K/V

@@ -176,6 +176,14 @@ pa_status pa_stream_read(const void* buf, size_t bytes, int blocks, uint32_t* si
 pa_status pa_stream_read_ex(const void* buf, size_t bytes, int blocks, int threads_per_block, int unroll,
                             int nontemporal, uint32_t* sink, void* stream);
 
+/* The same read with each wave streaming one contiguous span: `bytes` splits
+ * into blocks x threads/64 equal spans, each a multiple of unroll KiB
+ * (unroll in {8, 16}, threads in {256, 512}); non-temporal 16 B loads. The
+ * highest-rate read shape on MI355X, reported as the read ceiling beside
+ * bench_decode.cu:224-240's grid-stride copy rows. */
+pa_status pa_stream_read_chunked(const void* buf, size_t bytes, int blocks, int threads_per_block, int unroll,
+                                 uint32_t* sink, void* stream);
+
 /* Streaming write of the byte `value` over `bytes` (a multiple of 16): the
  * write-side counterpart of pa_stream_read (bench_decode.cu:61-68 fills the
  * bench inputs; here it is a write of known size for counter calibration). */

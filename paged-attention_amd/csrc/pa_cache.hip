@@ -5,6 +5,7 @@
 //                        new block-table entries and lengths, in one launch
 //   gather_kernel        block-table resolution probe (the decode kernel's row address function)
 //   stream_read_kernel   streaming read: cache flush and plain-copy ceiling (bench_decode.cu:70-78)
+//   stream_read_chunked_kernel  the same read with one contiguous span per wave (best read rate)
 //   fill_bytes_kernel    streaming write of a byte value (bench_decode.cu:61-68's fill role; the
 //                        write-side counterpart of the copy ceiling)
 
@@ -230,6 +231,30 @@ __global__ __launch_bounds__(512) void stream_read_kernel(const u32x4* __restric
     if (acc == 0x12345678u) *sink = acc;   // keeps the loads alive
 }
 
+// Streaming read where each wave reads its own contiguous `per`-byte span
+// (U KiB per trip, 16 B per lane per KiB, non-temporal raw buffer loads):
+// the access shape that reaches the highest read rate on this part, since a
+// wave's requests stay within few DRAM pages. `per` is a multiple of U KiB.
+template <int U>
+__global__ __launch_bounds__(512) void stream_read_chunked_kernel(const unsigned char* __restrict__ x, size_t per,
+                                                                  uint32_t* sink) {
+    const int    lane = threadIdx.x & 63;
+    const size_t wave = (static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x) >> 6;
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<unsigned char*>(x + wave * per), 0, static_cast<int>(per), 0x00020000);
+    uint32_t acc = 0;
+    for (size_t off = 0; off < per; off += U * 1024) {
+        u32x4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+            v[u] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                 r, static_cast<int>(off) + u * 1024 + 16 * lane, 0, 2));
+#pragma unroll
+        for (int u = 0; u < U; ++u) acc ^= v[u][0] ^ v[u][1] ^ v[u][2] ^ v[u][3];
+    }
+    if (acc == 0x12345678u) *sink = acc;
+}
+
 // Streaming write: every 16-byte word of x gets `word` repeated.
 __global__ __launch_bounds__(256) void fill_bytes_kernel(u32x4* __restrict__ x, size_t n, uint32_t word) {
     const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
@@ -289,6 +314,23 @@ hipError_t launch_fill_bytes(void* buf, size_t bytes, int value, hipStream_t s) 
     const int blocks = static_cast<int>(want < 16384 ? want : 16384);
     hipLaunchKernelGGL(fill_bytes_kernel, dim3(blocks), dim3(256), 0, s, static_cast<u32x4*>(buf), n,
                        b | (b << 8) | (b << 16) | (b << 24));
+    return hipGetLastError();
+}
+
+hipError_t launch_stream_read_chunked(const void* buf, size_t bytes, int blocks, int threads, int unroll,
+                                     uint32_t* sink, hipStream_t s) {
+    if (threads != 256 && threads != 512) throw std::invalid_argument("stream_read_chunked: threads must be 256 or 512");
+    if (unroll != 8 && unroll != 16) throw std::invalid_argument("stream_read_chunked: unroll must be 8 or 16");
+    const size_t waves = static_cast<size_t>(blocks) * (threads / 64);
+    const size_t trip  = static_cast<size_t>(unroll) * 1024;
+    if (blocks <= 0 || bytes % (waves * trip) != 0 || bytes / waves > static_cast<size_t>(INT32_MAX))
+        throw std::invalid_argument("stream_read_chunked: bytes must split into equal spans of whole trips per wave");
+    const auto*  x   = static_cast<const unsigned char*>(buf);
+    const size_t per = bytes / waves;
+    if (unroll == 8)
+        hipLaunchKernelGGL(stream_read_chunked_kernel<8>, dim3(blocks), dim3(threads), 0, s, x, per, sink);
+    else
+        hipLaunchKernelGGL(stream_read_chunked_kernel<16>, dim3(blocks), dim3(threads), 0, s, x, per, sink);
     return hipGetLastError();
 }
 

@@ -638,6 +638,15 @@ pa_status pa_stream_read(const void* buf, size_t bytes, int blocks, uint32_t* si
     return pa_stream_read_ex(buf, bytes, blocks, 256, 1, 0, sink, stream);
 }
 
+pa_status pa_stream_read_chunked(const void* buf, size_t bytes, int blocks, int threads, int unroll, uint32_t* sink,
+                                 void* stream) {
+    return guarded([&] {
+        if (!buf || !sink) throw std::invalid_argument("stream_read_chunked: null pointer");
+        pa::hip_check(pa::launch_stream_read_chunked(buf, bytes, blocks, threads, unroll, sink, as_stream(stream)),
+                      "stream_read_chunked launch");
+    });
+}
+
 pa_status pa_stream_read_ex(const void* buf, size_t bytes, int blocks, int threads, int unroll, int nontemporal,
                             uint32_t* sink, void* stream) {
     return guarded([&] {

@@ -61,7 +61,7 @@
 #endif
 // Steps of K/V in flight per wave.
 #ifndef PA_FP16_DEPTH
-#define PA_FP16_DEPTH 4
+#define PA_FP16_DEPTH 2
 #endif
 #ifndef PA_FP8_DEPTH
 #define PA_FP8_DEPTH 3
@@ -681,32 +681,38 @@ void decode_split_kernel_fp8(const pa_decode_params p, int page_shift) {
 }
 
 // ---------------------------------------------------------------------------
-// Merge (decode_kernels.cuh:409-432): one block per (query head, batch row) of
-// a row split over n > 1 segments. Pass 1 takes the maximum base-2 LSE; pass 2
-// has each wave accumulate sum_s 2^(lse_s - max) o_s over every WAVES-th
-// segment (two dims per lane, loads unrolled), and the waves combine in LDS.
-template <int G, int WAVES>
+// Merge (decode_kernels.cuh:409-432): one block per (query head, batch row,
+// DS-dim slice) of a row split over n > 1 segments; slicing the 128 dims over
+// 128 / DS blocks spreads a few long rows (C5: 32 rows of 256 segments) over
+// every CU, since one CU streams only ~25 GB/s. Pass 1 takes the maximum base-2
+// LSE over the row's segments. Pass 2: DS / 4 lanes cover a segment's slice
+// (4 dims each, one 16-byte load), so a wave covers 256 / DS segments at a
+// time; each lane accumulates sum_s 2^(lse_s - max) o_s and the weight sum
+// over its segments, lanes of the same dims combine by shuffles, waves in LDS.
+template <int G, int WAVES, int DS>
 __global__ __launch_bounds__(64 * WAVES) void decode_merge_kernel(const pa_decode_params p) {
-    constexpr int NT = 64 * WAVES;
+    constexpr int NT  = 64 * WAVES;
+    constexpr int LPS = DS / 4;      // lanes per segment
+    constexpr int SPW = 64 / LPS;    // segments per wave per pass
     const int hqi  = blockIdx.x;
     const int b    = blockIdx.y;
+    const int d0   = blockIdx.z * DS;
     const int item = b * p.num_kv_heads + hqi / G;
     const int g    = hqi % G;
     const int s0 = p.item_seg_begin[item];
     const int n  = p.item_seg_begin[item + 1] - s0;
     if (n <= 1) return;
-    auto seg_of = [&](int i) -> size_t { return static_cast<size_t>(s0 + i); };
 
-    __shared__ float red[WAVES];
-    __shared__ float2 acc_lds[WAVES][64];
-    __shared__ float den_lds[WAVES];
+    __shared__ float  red[WAVES];
+    __shared__ float4 acc_lds[WAVES][LPS];
+    __shared__ float  den_lds[WAVES];
 
     const int t    = threadIdx.x;
     const int lane = t & 63;
     const int wave = t >> 6;
 
     float mx = -INFINITY;
-    for (int i = t; i < n; i += NT) mx = fmaxf(mx, p.partial_lse[seg_of(i) * G + g]);
+    for (int i = t; i < n; i += NT) mx = fmaxf(mx, p.partial_lse[static_cast<size_t>(s0 + i) * G + g]);
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
     if (lane == 0) red[wave] = mx;
@@ -715,30 +721,47 @@ __global__ __launch_bounds__(64 * WAVES) void decode_merge_kernel(const pa_decod
 #pragma unroll
     for (int w = 1; w < WAVES; ++w) mx = fmaxf(mx, red[w]);
 
-    float n0 = 0.f, n1 = 0.f, den = 0.f;
-#pragma unroll 8
-    for (int i = wave; i < n; i += WAVES) {
-        const size_t sg  = seg_of(i);
+    const int dq = lane % LPS;       // which 4 dims of the slice
+    const int sl = lane / LPS;       // which segment of the wave's pass
+    float4 acc = {0.f, 0.f, 0.f, 0.f};
+    float  den = 0.f;
+#pragma unroll 4
+    for (int i = wave * SPW + sl; i < n; i += WAVES * SPW) {
+        const size_t sg  = static_cast<size_t>(s0 + i);
         const float  wgt = exp2_fast(p.partial_lse[sg * G + g] - mx);
-        const float2 o   = *reinterpret_cast<const float2*>(p.partial_out + (sg * G + g) * kHeadDim + 2 * lane);
-        n0 = fmaf(wgt, o.x, n0);
-        n1 = fmaf(wgt, o.y, n1);
+        const float4 o   = *reinterpret_cast<const float4*>(p.partial_out + (sg * G + g) * kHeadDim + d0 + 4 * dq);
+        acc.x = fmaf(wgt, o.x, acc.x);
+        acc.y = fmaf(wgt, o.y, acc.y);
+        acc.z = fmaf(wgt, o.z, acc.z);
+        acc.w = fmaf(wgt, o.w, acc.w);
         den += wgt;
     }
-    acc_lds[wave][lane] = float2{n0, n1};
+#pragma unroll
+    for (int o = LPS; o < 64; o <<= 1) {
+        acc.x += __shfl_xor(acc.x, o);
+        acc.y += __shfl_xor(acc.y, o);
+        acc.z += __shfl_xor(acc.z, o);
+        acc.w += __shfl_xor(acc.w, o);
+        den += __shfl_xor(den, o);
+    }
+    if (lane < LPS) acc_lds[wave][lane] = acc;
     if (lane == 0) den_lds[wave] = den;
     __syncthreads();
-    if (wave == 0) {
-        float a0 = 0.f, a1 = 0.f, d = 0.f;
+    if (wave == 0 && lane < LPS) {
+        float4 a = acc_lds[0][lane];
+        float  d = den_lds[0];
 #pragma unroll
-        for (int w = 0; w < WAVES; ++w) {
-            a0 += acc_lds[w][lane].x;
-            a1 += acc_lds[w][lane].y;
+        for (int w = 1; w < WAVES; ++w) {
+            a.x += acc_lds[w][lane].x;
+            a.y += acc_lds[w][lane].y;
+            a.z += acc_lds[w][lane].z;
+            a.w += acc_lds[w][lane].w;
             d += den_lds[w];
         }
-        const f16x2 h2 = {static_cast<_Float16>(a0 / d), static_cast<_Float16>(a1 / d)};
-        *reinterpret_cast<uint32_t*>(p.out + (static_cast<size_t>(b) * p.num_q_heads + hqi) * kHeadDim + 2 * lane) =
-            __builtin_bit_cast(uint32_t, h2);
+        const f16x2 lo = {static_cast<_Float16>(a.x / d), static_cast<_Float16>(a.y / d)};
+        const f16x2 hi = {static_cast<_Float16>(a.z / d), static_cast<_Float16>(a.w / d)};
+        *reinterpret_cast<u32x2*>(p.out + (static_cast<size_t>(b) * p.num_q_heads + hqi) * kHeadDim + d0 + 4 * dq) =
+            u32x2{__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi)};
     }
 }
 
@@ -787,17 +810,29 @@ hipError_t launch_split_e(const pa_decode_params& p, int group, hipStream_t s) {
     throw std::invalid_argument("unsupported GQA group size " + std::to_string(group));
 }
 
+template <int G, int DS>
+hipError_t launch_merge_gd(const pa_decode_params& p, hipStream_t s) {
+    const dim3 grid(p.num_q_heads, p.batch, kHeadDim / DS);
+    constexpr int SPW = 256 / DS;    // segments one wave covers per pass
+    const int m = p.max_item_segments;
+    if (m > 0 && m <= 2 * SPW)
+        hipLaunchKernelGGL((decode_merge_kernel<G, 1, DS>), grid, dim3(64), 0, s, p);
+    else if (m > 0 && m <= 8 * SPW)
+        hipLaunchKernelGGL((decode_merge_kernel<G, 4, DS>), grid, dim3(256), 0, s, p);
+    else
+        hipLaunchKernelGGL((decode_merge_kernel<G, 16, DS>), grid, dim3(1024), 0, s, p);
+    return hipGetLastError();
+}
+
+// Dim slices per (head, row): enough blocks to reach every CU when few rows
+// are split (at least ~1024 blocks), whole rows when many are.
 template <int G>
 hipError_t launch_merge_g(const pa_decode_params& p, hipStream_t s) {
-    const dim3 grid(p.num_q_heads, p.batch);
-    const int m = p.max_item_segments;
-    if (m > 0 && m <= 4)
-        hipLaunchKernelGGL((decode_merge_kernel<G, 1>), grid, dim3(64), 0, s, p);
-    else if (m > 0 && m <= 16)
-        hipLaunchKernelGGL((decode_merge_kernel<G, 4>), grid, dim3(256), 0, s, p);
-    else
-        hipLaunchKernelGGL((decode_merge_kernel<G, 16>), grid, dim3(1024), 0, s, p);
-    return hipGetLastError();
+    const long pairs = static_cast<long>(p.batch) * p.num_q_heads;
+    if (pairs >= 1024) return launch_merge_gd<G, 128>(p, s);
+    if (pairs >= 512) return launch_merge_gd<G, 64>(p, s);
+    if (pairs >= 256) return launch_merge_gd<G, 32>(p, s);
+    return launch_merge_gd<G, 16>(p, s);
 }
 
 int checked_group(const pa_decode_params& p) {

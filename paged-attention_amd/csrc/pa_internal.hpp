@@ -25,7 +25,10 @@ inline void hip_check(hipError_t e, const char* what) {
 
 constexpr int kHeadDim     = 128;   // the only head_dim the path supports (decode.cu:31-38)
 constexpr int kGroupTokens = 16;    // tokens per MFMA step of the decode kernel
-constexpr int kBlockUnits  = 8;     // work units (waves) per block of the decode kernel
+#ifndef PA_BLOCK_UNITS
+#define PA_BLOCK_UNITS 8
+#endif
+constexpr int kBlockUnits  = PA_BLOCK_UNITS;   // work units (waves) per block of the decode kernel
 
 inline void check_kv_dtype(int dtype) {
     if (dtype != PA_KV_FP16 && dtype != PA_KV_FP8_E4M3)
@@ -68,6 +71,8 @@ hipError_t launch_append_batch(int dtype, const AppendBatch& a, hipStream_t s);
 hipError_t launch_gather(int dtype, const void* cache, const int32_t* bt_row, int hkv,
                          int page_size, int kv_head, int len, void* out, hipStream_t s);
 hipError_t launch_fill_bytes(void* buf, size_t bytes, int value, hipStream_t s);
+hipError_t launch_stream_read_chunked(const void* buf, size_t bytes, int blocks, int threads, int unroll,
+                                     uint32_t* sink, hipStream_t s);
 hipError_t launch_stream_read(const void* buf, size_t bytes, int blocks, int threads, int unroll, bool nt,
                               uint32_t* sink, hipStream_t s);
 

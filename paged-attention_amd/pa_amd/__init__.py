@@ -9,7 +9,7 @@ from . import _lib
 from ._lib import DecodeParams, CacheConfig, PaError, InvalidArgument, LengthError, DeviceError
 from .core import (FP16, FP8_E4M3, DecodePlan, DevicePlan, PagePool, PagedKVCache, make_plan,
                    make_plan_tiled, paged_decode, decode_split, decode_merge, append_quantize,
-                   gather_kv, stream_read, fill_bytes, tile_tokens, wave_ctas, default_ctas, kv_dtype_bytes,
+                   gather_kv, stream_read, stream_read_chunked, fill_bytes, tile_tokens, wave_ctas, default_ctas, kv_dtype_bytes,
                    kv_dtype_name, sm_scale)
 
 
@@ -23,6 +23,6 @@ __all__ = [
     "_lib", "DecodeParams", "CacheConfig", "PaError", "InvalidArgument", "LengthError",
     "DeviceError", "FP16", "FP8_E4M3", "DecodePlan", "DevicePlan", "PagePool", "PagedKVCache",
     "make_plan", "make_plan_tiled", "paged_decode", "decode_split", "decode_merge",
-    "append_quantize", "gather_kv", "stream_read", "fill_bytes", "tile_tokens", "wave_ctas", "default_ctas",
+    "append_quantize", "gather_kv", "stream_read", "stream_read_chunked", "fill_bytes", "tile_tokens", "wave_ctas", "default_ctas",
     "kv_dtype_bytes", "kv_dtype_name", "sm_scale", "Decoder",
 ]

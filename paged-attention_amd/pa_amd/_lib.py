@@ -128,6 +128,7 @@ SIGNATURES: dict[str, tuple] = {
     "pa_gather_kv": (_I, [_I, _P, _P, _I, _I, _I, _I, _I, _P, _P]),
     "pa_stream_read": (_I, [_P, _S, _I, _P, _P]),
     "pa_stream_read_ex": (_I, [_P, _S, _I, _I, _I, _I, _P, _P]),
+    "pa_stream_read_chunked": (_I, [_P, _S, _I, _I, _I, _P, _P]),
     "pa_fill_bytes": (_I, [_P, _S, _I, _P]),
     "pa_pool_create": (_I, [_I, _I, _I, _I, _PP]),
     "pa_pool_destroy": (None, [_P]),

@@ -36,6 +36,7 @@ import sys
 import numpy as np
 
 from . import core
+from ._lib import InvalidArgument
 
 PEAK_GBPS = 8000.0
 FLUSH_BYTES = 1 << 30
@@ -161,7 +162,8 @@ def time_cold(flusher: Flusher | None, iters: int, fn) -> list[float]:
 
 def copy_rows(cus: int, iters: int = 10, nbytes: int = 4 << 30) -> list[dict]:
     """bench_decode.cu:224-240 plus unrolled and non-temporal variants of the
-    same 16 B/lane read: one row per (grid, block, unroll, nt)."""
+    same 16 B/lane read: one row per (grid, block, unroll, nt); then the
+    chunked read (one contiguous span per wave), the best read shape."""
     import torch
     buf = torch.ones(nbytes, dtype=torch.uint8, device="cuda")
     sink = torch.zeros(1, dtype=torch.int32, device="cuda")
@@ -183,6 +185,24 @@ def copy_rows(cus: int, iters: int = 10, nbytes: int = 4 << 30) -> list[dict]:
                 ms.append(a.elapsed_time(b))
         med = statistics.median(ms)
         rows.append({"kernel": f"read_{blocks}x{threads}_u{unroll}{'_nt' if nt else ''}", "bytes": nbytes,
+                     "time_us": med * 1e3, "gbps": nbytes / (med * 1e-3) / 1e9})
+    for mult, unroll in ((1, 16), (2, 16), (4, 8)):
+        blocks = cus * mult
+        ms = []
+        try:
+            for i in range(iters + 2):
+                a = torch.cuda.Event(enable_timing=True)
+                b = torch.cuda.Event(enable_timing=True)
+                a.record(stream)
+                core.stream_read_chunked(buf, nbytes, blocks, sink, stream, threads=512, unroll=unroll)
+                b.record(stream)
+                b.synchronize()
+                if i >= 2:
+                    ms.append(a.elapsed_time(b))
+        except InvalidArgument:   # spans do not divide evenly on this CU count
+            continue
+        med = statistics.median(ms)
+        rows.append({"kernel": f"read_chunked_{blocks}x512_u{unroll}_nt", "bytes": nbytes,
                      "time_us": med * 1e3, "gbps": nbytes / (med * 1e-3) / 1e9})
     del buf
     return rows

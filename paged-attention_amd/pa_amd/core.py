@@ -191,6 +191,12 @@ def gather_kv(dtype: int, cache, block_table_row, num_kv_heads: int, head_dim: i
          page_size, kv_head, length, _ptr(out), _stream(stream))
 
 
+def stream_read_chunked(buf, nbytes: int, blocks: int, sink, stream=None, threads: int = 512,
+                        unroll: int = 16) -> None:
+    """Streaming read with one contiguous span per wave (the best read shape)."""
+    call("pa_stream_read_chunked", _ptr(buf), nbytes, blocks, threads, unroll, _ptr(sink), _stream(stream))
+
+
 def stream_read(buf, nbytes: int, blocks: int, sink, stream=None, threads: int = 256, unroll: int = 1,
                 nontemporal: bool = False) -> None:
     """bench_decode.cu:70-78 read_kernel (threads=256, unroll=1) and its unrolled variants."""
@@ -376,6 +382,6 @@ def sm_scale(head_dim: int) -> float:
 __all__ = [
     "FP16", "FP8_E4M3", "DecodeParams", "CacheConfig", "DecodePlan", "DevicePlan", "PagePool",
     "PagedKVCache", "make_plan", "make_plan_tiled", "paged_decode", "decode_split", "decode_merge",
-    "append_quantize", "gather_kv", "stream_read", "fill_bytes", "tile_tokens", "wave_ctas", "default_ctas",
+    "append_quantize", "gather_kv", "stream_read", "stream_read_chunked", "fill_bytes", "tile_tokens", "wave_ctas", "default_ctas",
     "kv_dtype_bytes", "kv_dtype_name", "sm_scale",
 ]
