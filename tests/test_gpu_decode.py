@@ -121,6 +121,93 @@ def test_append_fp8_bytes_exhaustive(scale):
     assert np.array_equal(vc.cpu().numpy(), cv)
 
 
+@pytest.mark.parametrize("lens", [[1024] * 4, [20000], [300, 4100, 17]], ids=["c1", "long", "ragged"])
+def test_graph_capture_replays_match_eager(lens):
+    """A decode step (PagedKVCache::run: split + merge launches) captured into
+    a HIP graph: every replay, with q rewritten and an eager decode of other
+    inputs between replays, equals the eager decode of the same q bitwise. The
+    launches record no memset nodes and keep no state between calls."""
+    import torch
+    hq, hkv = 32, 8
+    pages = [-(-L // 16) for L in lens]
+    cache = pa_amd.PagedKVCache(sum(pages) + 4, 16, hkv, D, len(lens), max(pages), pa_amd.FP16)
+    g = torch.Generator(device="cuda").manual_seed(3)
+    for L in lens:
+        s_ = cache.admit()
+        k = torch.randn(L, hkv, D, device="cuda", dtype=torch.float16, generator=g)
+        assert cache.append(s_, k, torch.randn_like(k), L)
+    cache.plan(list(range(len(lens))), hq)
+    q = torch.randn(len(lens), hq, D, device="cuda", dtype=torch.float16, generator=g)
+    out = torch.empty_like(q)
+    other_q = torch.randn(q.shape, device="cuda", dtype=q.dtype, generator=g)
+    other_out = torch.empty_like(q)
+    st = torch.cuda.Stream()
+    with torch.cuda.stream(st):
+        cache.run(q, out, st)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=st):
+            cache.run(q, out, torch.cuda.current_stream())
+        torch.cuda.synchronize()
+        for rep in range(4):
+            q.normal_(generator=g)
+            cache.run(q, out, st)                  # eager reference for this q
+            torch.cuda.synchronize()
+            ref = out.clone()
+            out.zero_()
+            graph.replay()
+            cache.run(other_q, other_out, st)      # eager work between replays
+            torch.cuda.synchronize()
+            assert torch.equal(out, ref), f"replay {rep} differs"
+    assert cache.last_plan().num_ctas > 0
+    cache.close()
+
+
+@pytest.mark.parametrize("fp8", DTYPES, ids=IDS)
+def test_cache_plan_subset_of_slots_in_any_order(fp8):
+    """PagedKVCache::plan(slots) (paged_kv_cache.cu:173-191): batch row i reads
+    cache slot slots[i]. A released and re-admitted slot, a subset of the
+    slots in a permuted order, and rows of different lengths; against the
+    oracle with the same slot mapping."""
+    import torch
+    dt = pa_amd.FP8_E4M3 if fp8 else pa_amd.FP16
+    hq, hkv, P = 32, 8, 16
+    scale = 4.0 / 448 if fp8 else 1.0
+    rng = np.random.default_rng(21)
+    lens = [100, 1, 700, 33, 2000, 16]
+    pages = sum(-(-L // P) for L in lens) + 8
+    cache = pa_amd.PagedKVCache(pages, P, hkv, D, 6, 2000 // P + 1, dt, scale, scale)
+    cache.shuffle_free_pages(4)
+    for L in lens:
+        s_ = cache.admit()
+        k = to_device(normal_f16(rng, (L, hkv, D)))
+        assert cache.append(s_, k, to_device(normal_f16(rng, (L, hkv, D))), L)
+    cache.release(1)
+    assert cache.admit() == 1
+    lens[1] = 50
+    assert cache.append(1, to_device(normal_f16(rng, (50, hkv, D))), to_device(normal_f16(rng, (50, hkv, D))), 50)
+    slots = [4, 1, 0, 5, 2]
+    q = normal_f16(rng, (len(slots), hq, D))
+    out = torch.empty((len(slots), hq, D), dtype=torch.float16, device="cuda")
+    cache.plan(slots, hq)
+    cache.run(to_device(q), out)
+    torch.cuda.synchronize()
+    p = cache.params()
+    eb = 1 if fp8 else 2
+    nbytes = pages * hkv * P * D * eb
+    view = (lambda a: a) if fp8 else (lambda a: a.view(np.uint16))
+    kc, vc = view(d2h(p.k_cache, nbytes)), view(d2h(p.v_cache, nbytes))
+    table = np.zeros((6, 2000 // P + 1), np.int32)
+    for s_ in range(6):
+        t = cache.block_table(s_)
+        table[s_, :len(t)] = t
+    ref = oracle.paged_decode(dt, q, kc, vc, table, np.asarray([lens[s_] for s_ in slots], np.int32), hq, hkv, D, P,
+                              scale, scale, slot_ids=np.asarray(slots, np.int32))
+    got = out.float().cpu().numpy()
+    assert float(np.max(np.abs(got - ref))) < TOL
+    cache.close()
+
+
 @pytest.mark.parametrize("fp8", DTYPES, ids=IDS)
 @pytest.mark.parametrize("page_size,chunk", [(16, 1), (16, 7), (5, 3), (64, 0)])
 def test_append_batch_decode_steps(fp8, page_size, chunk):
