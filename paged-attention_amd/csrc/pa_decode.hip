@@ -684,14 +684,13 @@ void decode_split_kernel_fp8(const pa_decode_params p, int page_shift) {
 // Merge (decode_kernels.cuh:409-432): one block per (query head, batch row,
 // DS-dim slice) of a row split over n > 1 segments; slicing the 128 dims over
 // 128 / DS blocks spreads a few long rows (C5: 32 rows of 256 segments) over
-// every CU, since one CU streams only ~25 GB/s. Pass 1 takes the maximum base-2
-// LSE over the row's segments. Pass 2: DS / 4 lanes cover a segment's slice
-// (4 dims each, one 16-byte load), so a wave covers 256 / DS segments at a
-// time; each lane accumulates sum_s 2^(lse_s - max) o_s and the weight sum
-// over its segments, lanes of the same dims combine by shuffles, waves in LDS.
+// every CU, since one CU streams only ~25 GB/s. DS / 4 lanes cover a segment's
+// slice (4 dims each, one 16-byte load), so a wave covers 256 / DS segments at
+// a time. A single pass over the segments with a running base-2 maximum per
+// lane (no separate pass for the maximum: one dependent round trip fewer);
+// lanes of the same dims combine by shuffles, waves in LDS.
 template <int G, int WAVES, int DS>
 __global__ __launch_bounds__(64 * WAVES) void decode_merge_kernel(const pa_decode_params p) {
-    constexpr int NT  = 64 * WAVES;
     constexpr int LPS = DS / 4;      // lanes per segment
     constexpr int SPW = 64 / LPS;    // segments per wave per pass
     const int hqi  = blockIdx.x;
@@ -703,60 +702,69 @@ __global__ __launch_bounds__(64 * WAVES) void decode_merge_kernel(const pa_decod
     const int n  = p.item_seg_begin[item + 1] - s0;
     if (n <= 1) return;
 
-    __shared__ float  red[WAVES];
     __shared__ float4 acc_lds[WAVES][LPS];
-    __shared__ float  den_lds[WAVES];
+    __shared__ float  den_lds[WAVES], max_lds[WAVES];
 
     const int t    = threadIdx.x;
     const int lane = t & 63;
     const int wave = t >> 6;
 
-    float mx = -INFINITY;
-    for (int i = t; i < n; i += NT) mx = fmaxf(mx, p.partial_lse[static_cast<size_t>(s0 + i) * G + g]);
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
-    if (lane == 0) red[wave] = mx;
-    __syncthreads();
-    mx = red[0];
-#pragma unroll
-    for (int w = 1; w < WAVES; ++w) mx = fmaxf(mx, red[w]);
-
+    // One pass: each lane keeps its own running maximum m of the base-2 LSEs
+    // it has seen and sum_s 2^(lse_s - m) o_s, sum_s 2^(lse_s - m), rescaled
+    // when m grows (an empty lane keeps m = -inf and contributes 0).
     const int dq = lane % LPS;       // which 4 dims of the slice
     const int sl = lane / LPS;       // which segment of the wave's pass
     float4 acc = {0.f, 0.f, 0.f, 0.f};
-    float  den = 0.f;
+    float  den = 0.f, m = -INFINITY;
 #pragma unroll 4
     for (int i = wave * SPW + sl; i < n; i += WAVES * SPW) {
         const size_t sg  = static_cast<size_t>(s0 + i);
-        const float  wgt = exp2_fast(p.partial_lse[sg * G + g] - mx);
+        const float  lse = p.partial_lse[sg * G + g];
         const float4 o   = *reinterpret_cast<const float4*>(p.partial_out + (sg * G + g) * kHeadDim + d0 + 4 * dq);
-        acc.x = fmaf(wgt, o.x, acc.x);
-        acc.y = fmaf(wgt, o.y, acc.y);
-        acc.z = fmaf(wgt, o.z, acc.z);
-        acc.w = fmaf(wgt, o.w, acc.w);
-        den += wgt;
+        const float  mn  = fmaxf(m, lse);
+        const float  f   = exp2_fast(m - mn);      // 0 while m = -inf
+        const float  wgt = exp2_fast(lse - mn);
+        acc.x = fmaf(wgt, o.x, acc.x * f);
+        acc.y = fmaf(wgt, o.y, acc.y * f);
+        acc.z = fmaf(wgt, o.z, acc.z * f);
+        acc.w = fmaf(wgt, o.w, acc.w * f);
+        den   = fmaf(den, f, wgt);
+        m     = mn;
     }
+    // Combine (m, den, acc) states: lanes of the same dims, then waves.
+    auto scale_to = [](float mi, float mt) { return mi == -INFINITY ? 0.f : exp2_fast(mi - mt); };
 #pragma unroll
     for (int o = LPS; o < 64; o <<= 1) {
-        acc.x += __shfl_xor(acc.x, o);
-        acc.y += __shfl_xor(acc.y, o);
-        acc.z += __shfl_xor(acc.z, o);
-        acc.w += __shfl_xor(acc.w, o);
-        den += __shfl_xor(den, o);
+        const float m2 = __shfl_xor(m, o);
+        const float mt = fmaxf(m, m2);
+        const float f1 = scale_to(m, mt), f2 = scale_to(m2, mt);
+        acc.x = acc.x * f1 + __shfl_xor(acc.x, o) * f2;
+        acc.y = acc.y * f1 + __shfl_xor(acc.y, o) * f2;
+        acc.z = acc.z * f1 + __shfl_xor(acc.z, o) * f2;
+        acc.w = acc.w * f1 + __shfl_xor(acc.w, o) * f2;
+        den   = den * f1 + __shfl_xor(den, o) * f2;
+        m     = mt;
     }
     if (lane < LPS) acc_lds[wave][lane] = acc;
-    if (lane == 0) den_lds[wave] = den;
+    if (lane == 0) {
+        den_lds[wave] = den;
+        max_lds[wave] = m;
+    }
     __syncthreads();
     if (wave == 0 && lane < LPS) {
-        float4 a = acc_lds[0][lane];
-        float  d = den_lds[0];
+        float mt = max_lds[0];
 #pragma unroll
-        for (int w = 1; w < WAVES; ++w) {
-            a.x += acc_lds[w][lane].x;
-            a.y += acc_lds[w][lane].y;
-            a.z += acc_lds[w][lane].z;
-            a.w += acc_lds[w][lane].w;
-            d += den_lds[w];
+        for (int w = 1; w < WAVES; ++w) mt = fmaxf(mt, max_lds[w]);
+        float4 a = {0.f, 0.f, 0.f, 0.f};
+        float  d = 0.f;
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w) {
+            const float f = scale_to(max_lds[w], mt);
+            a.x = fmaf(acc_lds[w][lane].x, f, a.x);
+            a.y = fmaf(acc_lds[w][lane].y, f, a.y);
+            a.z = fmaf(acc_lds[w][lane].z, f, a.z);
+            a.w = fmaf(acc_lds[w][lane].w, f, a.w);
+            d   = fmaf(den_lds[w], f, d);
         }
         const f16x2 lo = {static_cast<_Float16>(a.x / d), static_cast<_Float16>(a.y / d)};
         const f16x2 hi = {static_cast<_Float16>(a.z / d), static_cast<_Float16>(a.w / d)};
