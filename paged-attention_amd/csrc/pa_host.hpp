@@ -1,0 +1,150 @@
+#pragma once
+// Host-side state behind the C ABI of libpa_decode.so (plans, device plans, the
+// page pool, the paged cache) and the helpers the C entry points share. Internal
+// to the library; the public interface is include/pa_decode.h.
+
+#include "pa_decode.h"
+#include "pa_internal.hpp"
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <new>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+// Host copy of a schedule (decode.hpp:21-27 DecodePlan).
+struct pa_plan {
+    int num_ctas = 0;
+    int tile     = 0;
+    int items    = 0;
+    std::vector<int32_t> segments;        // [n][4] = (row, kv head, tok_begin, tok_end)
+    std::vector<int32_t> cta_seg_begin;   // [num_ctas + 1]
+    std::vector<int32_t> item_seg_begin;  // [items + 1]
+};
+
+// Device copy of a plan plus the partial workspace (decode.hpp:44-63).
+struct pa_device_plan {
+    int32_t* segments       = nullptr;
+    int32_t* cta_seg_begin  = nullptr;
+    int32_t* item_seg_begin = nullptr;
+    float*   partial_out    = nullptr;
+    float*   partial_lse    = nullptr;
+    size_t   seg_cap = 0, cta_cap = 0, item_cap = 0, part_cap = 0;
+    int      num_ctas    = 0;
+    int      needs_merge = 0;
+    int      max_item_segments = 0;
+    bool     block_merge = false;
+};
+
+// Host page allocator and per-slot block tables (paged_kv_cache.hpp:89-92).
+struct pa_pool {
+    int page_size          = 0;
+    int max_slots          = 0;
+    int max_pages_per_slot = 0;
+    std::vector<int32_t>              free_pages;   // back() is handed out next
+    std::vector<std::vector<int32_t>> tables;
+    std::vector<int32_t>              seq_lens;
+    std::vector<char>                 occupied;
+};
+
+// One host-to-device staging buffer of the batched append: pinned host ints,
+// their device copy, and an event recorded after the kernel that reads them.
+struct pa_stage {
+    int32_t*   host = nullptr;
+    int32_t*   dev  = nullptr;
+    size_t     cap  = 0;   // int32 elements
+    hipEvent_t done = nullptr;
+};
+
+struct pa_cache {
+    pa_cache_config cfg{};
+    pa_pool         pool;
+    void*           d_k          = nullptr;
+    void*           d_v          = nullptr;
+    int32_t*        d_table      = nullptr;   // [max_slots][max_pages_per_slot]
+    int32_t*        d_seq_lens   = nullptr;   // [max_slots]
+    int32_t*        d_slot_ids   = nullptr;
+    size_t          slot_ids_cap = 0;
+    pa_plan         plan;
+    pa_device_plan  dplan;
+    int             plan_batch = 0;
+    int             plan_hq    = 0;
+    pa_stage        stage[2];   // used in turn, so one batch may still be in flight while the next is staged
+    int             stage_next = 0;
+};
+
+namespace pa::host {
+
+// The message behind this thread's last non-OK status (pa_last_error).
+extern thread_local std::string g_last_error;
+
+// Runs f and maps its exception to a status (pa_decode.h): the reference's
+// std::invalid_argument / std::length_error, and device errors.
+template <class F>
+inline pa_status guarded(F&& f) {
+    try {
+        f();
+        return PA_OK;
+    } catch (const std::invalid_argument& e) {
+        g_last_error = e.what();
+        return PA_ERR_INVALID_ARGUMENT;
+    } catch (const std::length_error& e) {
+        g_last_error = e.what();
+        return PA_ERR_LENGTH;
+    } catch (const pa::DeviceError& e) {
+        g_last_error = e.what();
+        return PA_ERR_DEVICE;
+    } catch (const std::bad_alloc&) {
+        g_last_error = "host allocation failed";
+        return PA_ERR_DEVICE;
+    } catch (const std::exception& e) {
+        g_last_error = e.what();
+        return PA_ERR_DEVICE;
+    }
+}
+
+inline hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
+
+// Grow-only device buffer refreshed from host data on `s`.
+template <class T>
+inline void upload_grow(T*& dst, size_t& cap, const T* src, size_t n, hipStream_t s) {
+    if (n > cap) {
+        pa::hip_check(hipFree(dst), "hipFree");
+        dst = nullptr;
+        pa::hip_check(hipMalloc(reinterpret_cast<void**>(&dst), sizeof(T) * n), "hipMalloc");
+        cap = n;
+    }
+    if (n) pa::hip_check(hipMemcpyAsync(dst, src, sizeof(T) * n, hipMemcpyHostToDevice, s), "hipMemcpyAsync");
+}
+
+// ---- planner and device plan (pa_plan.cpp)
+void check_dtype(int dtype);
+void make_plan_impl(pa_plan& plan, int dtype, const int32_t* lens, int batch, int hq, int hkv, int hd,
+                    int num_ctas);
+void device_plan_upload(pa_device_plan& dp, const pa_plan& plan, int group, int head_dim, hipStream_t s);
+void device_plan_bind(const pa_device_plan& dp, pa_decode_params& p);
+void device_plan_free(pa_device_plan& dp);
+void decode_impl(int dtype, const pa_decode_params& p, hipStream_t s, bool split, bool merge);
+
+// ---- page pool (pa_pool.cpp)
+// Entry i of a batched append: the slot's length before it, and the table
+// entries it added.
+struct reserve_entry {
+    int old_len   = 0;
+    int first_new = 0;
+    int num_new   = 0;
+};
+
+void pool_init(pa_pool& pool, int num_pages, int page_size, int max_slots, int max_pages_per_slot);
+bool slot_ok(const pa_pool& pool, int slot);
+int  pool_admit(pa_pool& pool);
+// Append bookkeeping: false (nothing changed) when out of pages.
+bool pool_reserve(pa_pool& pool, int slot, int n, int& first_new, int& num_new);
+bool pool_reserve_batch(pa_pool& pool, const int32_t* slots, const int32_t* counts, int n,
+                        std::vector<reserve_entry>* entries);
+void pool_release(pa_pool& pool, int slot);
+
+}  // namespace pa::host

@@ -1,5 +1,6 @@
-// Internal interface between the C-ABI host layer (pa_capi.cpp) and the
-// gfx950 kernels (pa_kernels.hip). Not installed; callers use pa_decode.h.
+// Internal interface between the C-ABI host layer (pa_plan.cpp, pa_pool.cpp,
+// pa_kvcache.cpp) and the gfx950 kernels (pa_decode.hip, pa_cache.hip). Not
+// installed; callers use pa_decode.h.
 #pragma once
 
 #include "pa_decode.h"
