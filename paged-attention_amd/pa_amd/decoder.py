@@ -30,6 +30,7 @@ class Decoder:
         self._page = int(page_size)
         self._dtype = core.FP8_E4M3 if fp8 else core.FP16
         self._batch = 0
+        self._table_cols = 0   # block-table columns the plan's longest row needs
         self._plan: core.DecodePlan | None = None
         self._device_plan = core.DevicePlan()
 
@@ -39,6 +40,7 @@ class Decoder:
                  "seq_lens must be a CPU int32 tensor")
         lens = seq_lens.contiguous().numpy()
         self._plan = core.make_plan(self._dtype, lens, self._hq, self._hkv, self._dim, num_ctas)
+        self._table_cols = int((int(lens.max()) + self._page - 1) // self._page) if lens.size else 0
         self._device_plan.upload(self._plan, self._hq // self._hkv, self._dim,
                                  torch.cuda.current_stream())
         self._batch = int(lens.shape[0])
@@ -53,6 +55,19 @@ class Decoder:
                  "caches and block_table must be contiguous")
         _require(q.size(0) == self._batch, "q batch does not match the plan")
         _require(block_table.dtype == torch.int32, "block_table must be int32")
+        # Shape checks beyond the reference's: a mismatch here would otherwise
+        # become out-of-range device reads.
+        _require(tuple(q.shape[1:]) == (self._hq, self._dim), "q must be [batch, num_q_heads, head_dim]")
+        elem = 2 if self._dtype == core.FP16 else 1
+        for name, c in (("k_cache", k_cache), ("v_cache", v_cache)):
+            _require(c.is_cuda and c.dim() == 4 and tuple(c.shape[1:]) == (self._hkv, self._page, self._dim)
+                     and c.element_size() == elem,
+                     f"{name} must be a CUDA [pages, num_kv_heads, page_size, head_dim] tensor of "
+                     f"{'fp16' if elem == 2 else 'one-byte FP8'} elements")
+        _require(block_table.is_cuda and block_table.dim() == 2 and block_table.size(0) >= self._batch
+                 and block_table.size(1) >= self._table_cols,
+                 "block_table must be a CUDA [batch, >= ceil(max seq_len / page_size)] tensor")
+        _require(seq_lens_dev.is_cuda and seq_lens_dev.dtype == torch.int32, "seq_lens must be a CUDA int32 tensor")
         out = torch.empty_like(q)
         p = DecodeParams()
         p.q = q.data_ptr()

@@ -461,6 +461,25 @@ def test_decoder_ragged_config4_subset():
     assert err < TOL, err
 
 
+def test_decoder_rejects_inconsistent_inputs():
+    """Decoder.run raises RuntimeError (the reference's TORCH_CHECK) for inputs
+    whose shapes or types do not match the plan, before any launch."""
+    import torch
+    q, k, v, table, ks, vs = _paged_inputs(2, [40, 17], 32, 8, 16, False, 0)
+    dec = pa_amd.Decoder(32, 8, D, 16, False)
+    lens = torch.tensor([40, 17], dtype=torch.int32)
+    dec.plan(lens, 0)
+    good = dict(q=q, k_cache=k, v_cache=v, block_table=table, seq_lens_dev=lens.cuda(), k_scale=1.0, v_scale=1.0)
+    dec.run(**good)
+    bad = [dict(q=q.float()), dict(q=q[:1].contiguous()), dict(q=q.view(2, 8, 4 * D)),
+           dict(k_cache=k.view(-1, 8, 8, D)), dict(v_cache=v.view(torch.uint8)), dict(block_table=table[:, :2].contiguous()),
+           dict(block_table=table.long()), dict(seq_lens_dev=lens), dict(k_cache=k.cpu())]
+    for change in bad:
+        with pytest.raises(RuntimeError):
+            dec.run(**{**good, **change})
+    torch.cuda.synchronize()
+
+
 @pytest.mark.parametrize("fp8", DTYPES, ids=IDS)
 def test_block_merge_and_merge_kernel_agree(fp8):
     """A plan whose split rows each lie in one block of 8 work units (8 units
