@@ -818,17 +818,17 @@ hipError_t launch_split_e(const pa_decode_params& p, int group, hipStream_t s) {
     throw std::invalid_argument("unsupported GQA group size " + std::to_string(group));
 }
 
+// About four segments per lane measured best (C1: 64 segments per row, one
+// wave; C5: 256, four waves); sixteen waves per block cost ~1 us more at C5.
 template <int G, int DS>
 hipError_t launch_merge_gd(const pa_decode_params& p, hipStream_t s) {
     const dim3 grid(p.num_q_heads, p.batch, kHeadDim / DS);
     constexpr int SPW = 256 / DS;    // segments one wave covers per pass
     const int m = p.max_item_segments;
-    if (m > 0 && m <= 2 * SPW)
+    if (m > 0 && m <= 4 * SPW)
         hipLaunchKernelGGL((decode_merge_kernel<G, 1, DS>), grid, dim3(64), 0, s, p);
-    else if (m > 0 && m <= 8 * SPW)
-        hipLaunchKernelGGL((decode_merge_kernel<G, 4, DS>), grid, dim3(256), 0, s, p);
     else
-        hipLaunchKernelGGL((decode_merge_kernel<G, 16, DS>), grid, dim3(1024), 0, s, p);
+        hipLaunchKernelGGL((decode_merge_kernel<G, 4, DS>), grid, dim3(256), 0, s, p);
     return hipGetLastError();
 }
 
