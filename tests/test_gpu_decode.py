@@ -461,6 +461,51 @@ def test_decoder_ragged_config4_subset():
     assert err < TOL, err
 
 
+@pytest.mark.parametrize("fp8", DTYPES, ids=IDS)
+def test_pages_beyond_4gib_of_pool(fp8):
+    """Pools larger than 4 GiB: the same sequence stored in the first pages
+    and in pages past the 4 GiB mark of each pool decodes to the same bits
+    (64-bit page offsets in every load path: power-of-two and per-lane)."""
+    import torch
+    hq, hkv = 32, 8
+    for P in (16, 5):
+        page_bytes = hkv * P * D * (1 if fp8 else 2)
+        pages = (4 << 30) // page_bytes + 4096                 # the last pages start past 4 GiB
+        dt = torch.uint8 if fp8 else torch.float16
+        k = torch.empty((pages, hkv, P, D), dtype=dt, device="cuda")
+        v = torch.empty_like(k)
+        L = 300
+        n = -(-L // P)
+        g = torch.Generator(device="cuda").manual_seed(P)
+        if fp8:
+            k[:n] = torch.randint(0, 0x7f, (n, hkv, P, D), device="cuda", generator=g, dtype=torch.int32).to(torch.uint8)
+            v[:n] = torch.randint(0, 0x7f, (n, hkv, P, D), device="cuda", generator=g, dtype=torch.int32).to(torch.uint8)
+        else:
+            k[:n] = torch.randn((n, hkv, P, D), device="cuda", generator=g, dtype=torch.float16)
+            v[:n] = torch.randn((n, hkv, P, D), device="cuda", generator=g, dtype=torch.float16)
+        high = torch.arange(pages - n, pages, device="cuda")
+        assert int(high[0]) * page_bytes >= (4 << 30)
+        q = torch.randn((1, hq, D), device="cuda", generator=g, dtype=torch.float16)
+        lens = torch.tensor([L], dtype=torch.int32)
+        dec = pa_amd.Decoder(hq, hkv, D, P, fp8)
+        dec.plan(lens, 0)
+
+        def run(table):
+            return dec.run(q, k, v, table.to(torch.int32).view(1, n).contiguous(), lens.cuda(), 0.01, 0.01)
+
+        outs = [run(torch.arange(n, device="cuda"))]
+        k[high] = k[:n].clone()
+        v[high] = v[:n].clone()
+        k[: pages - n].zero_()        # a wrapped 32-bit offset would now read zeros
+        v[: pages - n].zero_()
+        outs.append(run(high))
+        torch.cuda.synchronize()
+        assert torch.isfinite(outs[0].float()).all()
+        assert torch.equal(outs[0], outs[1]), f"page size {P}"
+        del k, v
+        torch.cuda.empty_cache()
+
+
 def test_decoder_rejects_inconsistent_inputs():
     """Decoder.run raises RuntimeError (the reference's TORCH_CHECK) for inputs
     whose shapes or types do not match the plan, before any launch."""
