@@ -462,6 +462,18 @@ def test_decoder_ragged_config4_subset():
 
 
 @pytest.mark.parametrize("fp8", DTYPES, ids=IDS)
+def test_many_short_rows(fp8):
+    """600 rows of 1..200 tokens: more (row, kv head) items (4800) than work
+    units, so units stream several whole items back to back and the pipeline
+    crosses many segment boundaries (segment-start q loads, finishes)."""
+    rng = np.random.default_rng(17)
+    lens = [int(x) for x in rng.integers(1, 201, size=600)]
+    err, dec = _decoder_case(len(lens), lens, fp8, threads=16)
+    assert dec.num_segments >= 600 * 8
+    assert err < TOL, err
+
+
+@pytest.mark.parametrize("fp8", DTYPES, ids=IDS)
 def test_pages_beyond_4gib_of_pool(fp8):
     """Pools larger than 4 GiB: the same sequence stored in the first pages
     and in pages past the 4 GiB mark of each pool decodes to the same bits
