@@ -461,6 +461,24 @@ def test_decoder_ragged_config4_subset():
     assert err < TOL, err
 
 
+@pytest.mark.parametrize("case", range(24))
+def test_seeded_random_configurations(case):
+    """24 seeded random combinations of dtype, GQA shape, page size, batch,
+    lengths (1 .. 3000), grid size and append chunking through the cache,
+    each against the oracle (bytes bit-exact, output within TOL)."""
+    rng = np.random.default_rng(1000 + case)
+    fp8 = bool(rng.integers(0, 2))
+    hq, hkv = [(8, 8), (8, 4), (16, 4), (32, 8), (8, 1), (32, 4)][int(rng.integers(0, 6))]
+    page = int(rng.choice([1, 2, 3, 5, 8, 16, 32, 64, 128]))
+    lens = [int(x) for x in rng.integers(1, 3001, size=int(rng.integers(1, 9)))]
+    ctas = int(rng.choice([0, 0, 1, 3, 17, 300]))
+    chunk = int(rng.choice([0, 0, 7, 64]))
+    err, _, plan = run_cache_case(fp8, hq, hkv, page, lens, num_ctas=ctas, chunk=chunk, seed=case,
+                                  shuffle_seed=case, batched=bool(rng.integers(0, 2)))
+    assert ctas == 0 or plan.num_ctas <= ctas
+    assert err < TOL, (err, fp8, hq, hkv, page, lens, ctas, chunk)
+
+
 @pytest.mark.parametrize("fp8", DTYPES, ids=IDS)
 def test_many_short_rows(fp8):
     """600 rows of 1..200 tokens: more (row, kv head) items (4800) than work
