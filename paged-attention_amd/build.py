@@ -80,5 +80,20 @@ def build(verbose: bool = False, defines: list[str] | None = None, lib: pathlib.
     return lib
 
 
+BENCH_SRC = PKG / "bench" / "bench_decode.cpp"
+BENCH_BIN = PKG / "bench" / "_build" / "bench_decode"
+
+
+def build_bench(verbose: bool = False) -> pathlib.Path:
+    """The native bench CLI (bench/bench_decode.cpp) against lib/libpa_decode.so."""
+    BENCH_BIN.parent.mkdir(parents=True, exist_ok=True)
+    cmd = [HIPCC, *COMMON, "-x", "hip", str(BENCH_SRC), f"-I{PKG / 'cpp'}", "-o", str(BENCH_BIN),
+           f"-L{LIB_DIR}", "-lpa_decode", f"-Wl,-rpath,$ORIGIN/../../lib"]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    _run(cmd)
+    return BENCH_BIN
+
+
 if __name__ == "__main__":
     print(build(verbose="-v" in sys.argv))

@@ -1,0 +1,59 @@
+"""The native bench CLI (paged-attention_amd/bench/bench_decode.cpp): the
+reference's bench/bench_decode.cu modes, flags and CSV columns."""
+
+import csv
+import io
+import pathlib
+import subprocess
+
+import pytest
+
+ROOT = pathlib.Path(__file__).resolve().parent.parent
+BIN = ROOT / "paged-attention_amd" / "bench" / "_build" / "bench_decode"
+GOLDEN = pathlib.Path(__file__).resolve().parent / "golden"
+HEADER = "gpu,dtype,batch,seq_len,hq,hkv,dim,page,ctas,segments,time_us,gbps,pct_peak"   # bench_decode.cu:194-196
+
+
+def _bin() -> pathlib.Path:
+    if not BIN.exists():
+        import importlib.util
+        spec = importlib.util.spec_from_file_location("pa_build", ROOT / "paged-attention_amd" / "build.py")
+        mod = importlib.util.module_from_spec(spec)
+        spec.loader.exec_module(mod)
+        mod.build_bench()
+    return BIN
+
+
+def _run(*args, timeout=300):
+    proc = subprocess.run([str(_bin()), *args], capture_output=True, text=True, timeout=timeout)
+    assert proc.returncode == 0, proc.stdout + proc.stderr
+    return proc.stdout
+
+
+def test_help_needs_no_device():
+    out = _run("--help")
+    assert out.startswith("usage: bench_decode sweep|ctas|pagesize|capacity|copy|single")
+
+
+@pytest.mark.gpu
+def test_single_row_columns():
+    out = _run("single", "--batch", "2", "--len", "300", "--iters", "3")
+    lines = out.strip().splitlines()
+    assert lines[0] == HEADER
+    row = next(csv.DictReader(io.StringIO(out)))
+    assert row["dtype"] == "fp16" and int(row["batch"]) == 2 and int(row["seq_len"]) == 300
+    assert float(row["time_us"]) > 0 and int(row["ctas"]) > 0 and int(row["segments"]) >= 16
+    out = _run("single", "--batch", "1", "--len", "1000", "--dtype", "fp8", "--page", "8", "--iters", "3")
+    row = next(csv.DictReader(io.StringIO(out)))
+    assert row["dtype"] == "fp8_e4m3" and row["page"] == "8"
+
+
+@pytest.mark.gpu
+def test_capacity_rows_match_reference():
+    """The capacity mode reproduces results/h100_capacity.csv (1 GiB budget)."""
+    out = _run("capacity")
+    got = list(csv.DictReader(io.StringIO(out)))
+    want = list(csv.DictReader(open(GOLDEN / "capacity_rows.csv")))
+    key = lambda r: (r["dtype"], r["layout"], r["actual_len"])   # noqa: E731
+    assert {key(r): (r["sequences"], r["bytes_per_seq"]) for r in got} == \
+        {key(r): (r["sequences"], r["bytes_per_seq"]) for r in want}
