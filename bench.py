@@ -15,9 +15,11 @@ Fields of the JSON line:
   value        algorithmic HBM GB/s of the whole step over the K timed steps,
                run back to back (bytes = 2*sum(L)*Hkv*D*e + 2*B*Hq*D*2 +
                sum(ceil(L/P))*4, bench_decode.cu:186-191)
-  roofline     the split kernel's algorithmic GB/s from HIP events around each
-               of K further launches (right after the timed steps), against
-               8 TB/s
+  roofline     the split kernel's algorithmic GB/s against 8 TB/s. Its
+               average duration comes from two HIP events bracketing the timed
+               steps on the kernels' stream when a step is the split kernel
+               alone (C2, C3), else from HIP events around each of K further
+               split launches (both figures are reported)
   cold         the reference's method: a 1 GiB flush before each run, HIP
                events around decode + merge, median of --cold-iters
   copy_ceiling best plain streaming read of 4 GiB (bench_decode.cu:224-240,
@@ -142,9 +144,10 @@ def cpu_baseline(s, name: str, budget_s: float, threads: int) -> dict:
 
 def time_steps(s, steps: int, warmup: int):
     """W untimed steps, then K timed steps back to back (wall clock between
-    synchronizations: the `value`), then K more split launches with HIP events
-    around each one on the stream the kernels run on (the kernel's average
-    launch duration for the roofline)."""
+    synchronizations: the `value`; two HIP events on the kernels' stream also
+    bracket the timed region), then K more split launches with HIP events
+    around each one on the same stream (the kernel's average launch duration
+    for the roofline; events between steps would stretch the timed steps)."""
     import torch
     stream = torch.cuda.current_stream()
     sh = stream.cuda_stream
@@ -153,10 +156,13 @@ def time_steps(s, steps: int, warmup: int):
         s.merge(sh)
     _barrier()
     torch.cuda.synchronize()
+    r0, r1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
+    r0.record(stream)
     for _ in range(steps):
         s.split(sh)
         s.merge(sh)
+    r1.record(stream)
     torch.cuda.synchronize()
     _barrier()
     wall = time.perf_counter() - t0
@@ -167,7 +173,7 @@ def time_steps(s, steps: int, warmup: int):
         b.record(stream)
         s.merge(sh)
     torch.cuda.synchronize()
-    return wall, [a.elapsed_time(b) for a, b in ev]
+    return wall, [a.elapsed_time(b) for a, b in ev], r0.elapsed_time(r1)
 
 
 CALIB_BYTES = 1 << 30   # size of the counter-calibration read and write kernels
@@ -290,11 +296,16 @@ def main() -> None:
     print(f"# setup done: {s.batch} seqs, {s.num_pages} pages, plan {s.plan.num_ctas} units / "
           f"{len(s.plan.segments)} segments", file=sys.stderr, flush=True)
 
-    wall, split_ms = time_steps(s, args.steps, args.warmup)
+    wall, split_ms, region_ms = time_steps(s, args.steps, args.warmup)
     nbytes = s.bytes()
     ms_per_step = wall * 1e3 / args.steps
     value = nbytes / (ms_per_step * 1e-3) / 1e9
-    split_avg = statistics.mean(split_ms)
+    # The split kernel's average duration: from the two events around the timed
+    # steps when a step is that kernel alone (no merge launch), else from the
+    # events around each of the K further split launches.
+    region_avg = region_ms / args.steps
+    only_split = s.params.needs_merge == 0
+    split_avg = region_avg if only_split else statistics.mean(split_ms)
     achieved = nbytes / (split_avg * 1e-3) / 1e9
     print(f"# timed {args.steps} steps: {ms_per_step * 1e3:.1f} us/step, split kernel {split_avg * 1e3:.1f} us avg",
           file=sys.stderr, flush=True)
@@ -338,6 +349,11 @@ def main() -> None:
             "frac": round(achieved / PEAK_GBPS, 4),
             "traffic": None,
             "avg_us": round(split_avg * 1e3, 2),
+            "avg_source": "timed-region events" if only_split else "per-launch events",
+            # HIP events bracketing the K timed steps on the kernels' stream:
+            # split + merge (if any) per step, launch gaps included.
+            "timed_region_avg_us": round(region_avg * 1e3, 2),
+            "per_launch_avg_us": round(statistics.mean(split_ms) * 1e3, 2),
         },
     }
     if traffic:
