@@ -9,6 +9,8 @@ with the oracle.
 import pathlib
 import sys
 
+import pytest
+
 ROOT = pathlib.Path(__file__).resolve().parent.parent
 for p in (ROOT, ROOT / "paged-attention_amd", ROOT / "tests"):
     if str(p) not in sys.path:
@@ -17,3 +19,15 @@ for p in (ROOT, ROOT / "paged-attention_amd", ROOT / "tests"):
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: runs HIP kernels on an MI355X (gfx950)")
+
+
+@pytest.fixture(scope="module")
+def gpu_device():
+    """GPU test modules use this (via pytestmark): a device must be present and
+    the HIP library loaded; nothing falls back to the CPU."""
+    import torch
+
+    import pa_amd
+    assert torch.cuda.is_available(), "GPU tests need a device"
+    pa_amd._lib.load()
+    yield

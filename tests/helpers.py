@@ -164,3 +164,59 @@ def _append_all(dt, K, V, ck, cv, bt_row, hkv, page_size, inv, fp8):
     vc = cv if fp8 else cv.view(np.uint16)
     oracle.append(dt, K.reshape(K.shape[0], -1), V.reshape(V.shape[0], -1), kc, vc, bt_row, 0, hkv, D,
                   page_size, inv, inv)
+
+
+def paged_inputs(batch, seq_lens, hq, hkv, page_size, fp8, seed):
+    """compare_flashinfer.py:80-97 style inputs: N(0,1) pools filled on the
+    device, a random page permutation as block table, per-tensor amax/448
+    scales with append-time quantization for FP8."""
+    import torch
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    pages_per = [math.ceil(L / page_size) for L in seq_lens]
+    num_pages = sum(pages_per)
+    max_pages = max(pages_per)
+    perm = torch.randperm(num_pages, device="cuda", generator=g).to(torch.int32)
+    table = torch.zeros(batch, max_pages, dtype=torch.int32, device="cuda")
+    off = 0
+    for b, n in enumerate(pages_per):
+        table[b, :n] = perm[off:off + n]
+        off += n
+    q = torch.randn(batch, hq, D, device="cuda", dtype=torch.float16, generator=g)
+    if not fp8:
+        k = torch.randn(num_pages, hkv, page_size, D, device="cuda", dtype=torch.float16, generator=g)
+        v = torch.randn(num_pages, hkv, page_size, D, device="cuda", dtype=torch.float16, generator=g)
+        return q, k, v, table, 1.0, 1.0
+    kc = torch.zeros(num_pages, hkv, page_size, D, device="cuda", dtype=torch.uint8)
+    vc = torch.zeros_like(kc)
+    srcs = []
+    for b, L in enumerate(seq_lens):
+        srcs.append((torch.randn(L, hkv, D, device="cuda", dtype=torch.float16, generator=g),
+                     torch.randn(L, hkv, D, device="cuda", dtype=torch.float16, generator=g)))
+    k_scale = max(float(s[0].abs().max()) for s in srcs) / 448.0
+    v_scale = max(float(s[1].abs().max()) for s in srcs) / 448.0
+    ik = float(np.float32(1.0) / np.float32(k_scale))
+    iv = float(np.float32(1.0) / np.float32(v_scale))
+    for b, (ks, vs) in enumerate(srcs):
+        pa_amd.append_quantize(pa_amd.FP8_E4M3, ks, vs, kc, vc, table[b], 0, seq_lens[b], hkv, D, page_size, ik, iv)
+    return q, kc, vc, table, k_scale, v_scale
+
+
+def decoder_case(batch, seq_lens, fp8, page_size=16, hq=32, hkv=8, seed=0, threads=16, rows=None):
+    """Decodes the whole batch on the GPU; checks every row against the oracle,
+    or only `rows` (a sample, for batches whose full oracle would take minutes)."""
+    import torch
+    q, k, v, table, ks, vs = paged_inputs(batch, seq_lens, hq, hkv, page_size, fp8, seed)
+    dec = pa_amd.Decoder(hq, hkv, D, page_size, fp8)
+    lens = torch.tensor(seq_lens, dtype=torch.int32)
+    dec.plan(lens, 0)
+    out = dec.run(q, k, v, table, lens.cuda(), ks, vs)
+    torch.cuda.synchronize()
+    dt = pa_amd.FP8_E4M3 if fp8 else pa_amd.FP16
+    kb = k.view(torch.uint8).cpu().numpy() if fp8 else k.view(torch.int16).cpu().numpy().view(np.uint16)
+    vb = v.view(torch.uint8).cpu().numpy() if fp8 else v.view(torch.int16).cpu().numpy().view(np.uint16)
+    sel = np.arange(batch) if rows is None else np.asarray(rows)
+    qb = q.view(torch.int16).cpu().numpy().view(np.uint16)[sel]
+    ref = oracle.paged_decode(dt, qb, kb, vb, table.cpu().numpy()[sel], np.asarray(seq_lens, np.int32)[sel], hq,
+                              hkv, D, page_size, ks, vs, threads=threads)
+    got = out.float().cpu().numpy()[sel]
+    return float(np.max(np.abs(got - ref))), dec
