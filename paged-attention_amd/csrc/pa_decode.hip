@@ -61,7 +61,7 @@
 #endif
 // Steps of K/V in flight per wave.
 #ifndef PA_FP16_DEPTH
-#define PA_FP16_DEPTH 2
+#define PA_FP16_DEPTH 1
 #endif
 #ifndef PA_FP8_DEPTH
 #define PA_FP8_DEPTH 3
