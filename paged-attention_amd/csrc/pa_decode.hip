@@ -168,73 +168,48 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, 
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, kBufferFlags);
 }
 
-// Block-level merge after the split loop. slot_item / slot_seg hold, per wave,
-// the (row, kv head) item and segment index of its first (slot 0) and last
-// (slot 1) segment when that segment is a split one, else item -1. Items appear
-// in block order (wave, slot) as contiguous runs (ignoring empty slots); the
-// wave holding a run's first slot merges the run: the base-2 LSE-weighted
-// average of the run's normalized partials (decode_kernels.cuh:409-432),
-// written as the fp16 output when the run is the whole row.
+// Block-level merge after the split loop. slot_item holds, per wave, the
+// (row, kv head) item of its first (slot 0) and last (slot 1) segment when that
+// segment is a split one, else -1; part / lse hold the slot's normalized
+// partial rows and base-2 LSEs, written to LDS by the wave that computed them.
+// Items appear in block order (wave, slot) as contiguous runs (ignoring empty
+// slots), and the planner turns this merge on only when every split row lies in
+// one block, so each run is a whole row. All threads of the block share the
+// outputs of a run (one head-dim element each): the base-2 LSE-weighted average
+// of the run's partials (decode_kernels.cuh:409-432), written as fp16.
 template <int G>
 __device__ __forceinline__ void block_merge(const pa_decode_params& p, const int (*slot_item)[2],
-                                            const int (*slot_seg)[2], int wave, int lane) {
+                                            const float (*part)[G * kHeadDim], const float (*lse)[G], int tid) {
     constexpr int NS = 2 * kWaves;
-    for (int sl = 0; sl < 2; ++sl) {
-        const int x = slot_item[wave][sl];
-        if (x < 0) continue;
-        int prev = -1;
-        for (int i = 2 * wave + sl - 1; i >= 0; --i)
-            if (slot_item[i >> 1][i & 1] >= 0) {
-                prev = slot_item[i >> 1][i & 1];
-                break;
-            }
-        if (prev == x) continue;   // another wave merges this run
-        int k = 0;
-        for (int i = 2 * wave + sl; i < NS; ++i) {
-            const int it = slot_item[i >> 1][i & 1];
-            if (it < 0) continue;
-            if (it != x) break;
-            ++k;
+    int i = 0;
+    while (i < NS) {
+        const int x = slot_item[i >> 1][i & 1];
+        if (x < 0) {
+            ++i;
+            continue;
         }
-        if (k != p.item_seg_begin[x + 1] - p.item_seg_begin[x]) continue;   // row spans blocks: merge kernel
+        int j = i + 1;
+        for (; j < NS; ++j) {
+            const int it = slot_item[j >> 1][j & 1];
+            if (it >= 0 && it != x) break;
+        }
         const int b = x / p.num_kv_heads, h = x - b * p.num_kv_heads;
-#pragma unroll
-        for (int t = lane; t < 16 * G; t += 64) {
-            const int g  = t >> 4;
-            const int ch = t & 15;
+        uint16_t* orow = p.out + (static_cast<size_t>(b) * p.num_q_heads + h * G) * kHeadDim;
+        for (int o = tid; o < G * kHeadDim; o += 64 * kWaves) {
+            const int g = o / kHeadDim;
             float mx = -INFINITY;
-            for (int i = 2 * wave + sl, j = 0; j < k; ++i) {
-                if (slot_item[i >> 1][i & 1] < 0) continue;
-                mx = fmaxf(mx, p.partial_lse[static_cast<size_t>(slot_seg[i >> 1][i & 1]) * G + g]);
-                ++j;
-            }
-            f32x4 a0 = {0.f, 0.f, 0.f, 0.f}, a1 = {0.f, 0.f, 0.f, 0.f};
-            float den = 0.f;
-            for (int i = 2 * wave + sl, j = 0; j < k; ++i) {
-                if (slot_item[i >> 1][i & 1] < 0) continue;
-                const size_t sg = static_cast<size_t>(slot_seg[i >> 1][i & 1]);
-                const float  w  = exp2_fast(p.partial_lse[sg * G + g] - mx);
-                const f32x4* o  = reinterpret_cast<const f32x4*>(p.partial_out + (sg * G + g) * kHeadDim + 8 * ch);
-                const f32x4  lo = o[0], hi = o[1];
-#pragma unroll
-                for (int jj = 0; jj < 4; ++jj) {
-                    a0[jj] = fmaf(w, lo[jj], a0[jj]);
-                    a1[jj] = fmaf(w, hi[jj], a1[jj]);
-                }
+            for (int s = i; s < j; ++s)
+                if (slot_item[s >> 1][s & 1] >= 0) mx = fmaxf(mx, lse[s][g]);
+            float a = 0.f, den = 0.f;
+            for (int s = i; s < j; ++s) {
+                if (slot_item[s >> 1][s & 1] < 0) continue;
+                const float w = exp2_fast(lse[s][g] - mx);
+                a = fmaf(w, part[s][o], a);
                 den += w;
-                ++j;
             }
-            const float inv = 1.0f / den;
-            u32x4 o;
-#pragma unroll
-            for (int jj = 0; jj < 2; ++jj) {
-                const f16x2 x0 = {static_cast<_Float16>(a0[2 * jj] * inv), static_cast<_Float16>(a0[2 * jj + 1] * inv)};
-                const f16x2 x1 = {static_cast<_Float16>(a1[2 * jj] * inv), static_cast<_Float16>(a1[2 * jj + 1] * inv)};
-                o[jj]     = __builtin_bit_cast(uint32_t, x0);
-                o[2 + jj] = __builtin_bit_cast(uint32_t, x1);
-            }
-            *reinterpret_cast<u32x4*>(p.out + (static_cast<size_t>(b) * p.num_q_heads + h * G + g) * kHeadDim + 8 * ch) = o;
+            orow[o] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(a * (1.0f / den)));
         }
+        i = j;
     }
 }
 
@@ -263,7 +238,10 @@ __device__ __forceinline__ void decode_split_body(const pa_decode_params& p, int
     using KRaw = std::conditional_t<KL == 16, u32x4, u32x2>;
 
     __shared__ __attribute__((aligned(16))) u32x4 q_lds[kWaves][16 * G];   // G heads x 256 B per wave
-    __shared__ int slot_item[kWaves][2], slot_seg[kWaves][2];                // split segments per wave
+    __shared__ int slot_item[kWaves][2];                                     // split segments per wave
+    // Partials of split segments for the block-level merge, slot 2 * wave + sl.
+    __shared__ __attribute__((aligned(16))) float part_lds[2 * kWaves][G * kHeadDim];
+    __shared__ float lse_lds[2 * kWaves][G];
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -367,8 +345,11 @@ __device__ __forceinline__ void decode_split_body(const pa_decode_params& p, int
             for (int hh = 0; hh < NH; ++hh) {
                 const int t  = L.tok + 16 * hh;          // first token of the half
                 const int bt = min(t, L.w - 1);          // a token of the sequence (pages stay in range)
-                const int nv = l_more ? max(0, min(16, L.w - t)) : 0;   // valid tokens of the half
-                const size_t row0 = static_cast<size_t>(pg[s][hh]) * page_bytes +
+                // The page and the valid tokens of the half are wave-uniform:
+                // said so, the K/V buffer resources stay in SGPRs (no per-load
+                // waterfall loop).
+                const int nv = __builtin_amdgcn_readfirstlane(l_more ? max(0, min(16, L.w - t)) : 0);
+                const size_t row0 = static_cast<size_t>(__builtin_amdgcn_readfirstlane(pg[s][hh])) * page_bytes +
                                     static_cast<uint32_t>((L.h * P + (bt & (P - 1))) * ROW);
                 const __amdgpu_buffer_rsrc_t krs = buffer_rsrc(kbase + row0, nv * ROW);
                 const __amdgpu_buffer_rsrc_t vrs = buffer_rsrc(vbase + row0, nv * ROW);
@@ -453,29 +434,32 @@ __device__ __forceinline__ void decode_split_body(const pa_decode_params& p, int
                                                           kHeadDim + 8 * c) = o;
                 }
             } else {
+                const int sl = C.seg == seg_begin ? 0 : 1;   // a unit's split segments are its first and last
 #pragma unroll
                 for (int i = 0; i < HW; ++i) {
                     const float lh  = head_pick<G>(inv_h, kb, i);
                     const float inv = p.v_scale / lh;
-                    float* prow = p.partial_out + (static_cast<size_t>(C.seg) * G + 4 * kb + i) * kHeadDim + 8 * c;
+                    const float ls  = head_pick<G>(m_h, kb, i) + __log2f(lh);
                     f32x4 lo, hi;
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
                         lo[j] = oacc[j][i] * inv;
                         hi[j] = oacc[4 + j][i] * inv;
                     }
-                    *reinterpret_cast<f32x4*>(prow)     = lo;
-                    *reinterpret_cast<f32x4*>(prow + 4) = hi;
-                    if (c == 0)
-                        p.partial_lse[static_cast<size_t>(C.seg) * G + 4 * kb + i] =
-                            head_pick<G>(m_h, kb, i) + __log2f(lh);
+                    if (merge_here) {
+                        float* lrow = &part_lds[2 * wave + sl][(4 * kb + i) * kHeadDim + 8 * c];
+                        *reinterpret_cast<f32x4*>(lrow)     = lo;
+                        *reinterpret_cast<f32x4*>(lrow + 4) = hi;
+                        if (c == 0) lse_lds[2 * wave + sl][4 * kb + i] = ls;
+                    } else {
+                        float* prow = p.partial_out + (static_cast<size_t>(C.seg) * G + 4 * kb + i) * kHeadDim + 8 * c;
+                        *reinterpret_cast<f32x4*>(prow)     = lo;
+                        *reinterpret_cast<f32x4*>(prow + 4) = hi;
+                        if (c == 0) p.partial_lse[static_cast<size_t>(C.seg) * G + 4 * kb + i] = ls;
+                    }
                 }
+                if (merge_here && lane == 0) slot_item[wave][sl] = C.b * hkv + C.h;
             }
-        }
-        if (!whole && merge_here && lane == 0) {
-            const int sl = C.seg == seg_begin ? 0 : 1;   // a unit's split segments are its first and last
-            slot_item[wave][sl] = C.b * hkv + C.h;
-            slot_seg[wave][sl]  = C.seg;
         }
         m_run = -INFINITY;
         l_run = 0.f;
@@ -663,7 +647,7 @@ __device__ __forceinline__ void decode_split_body(const pa_decode_params& p, int
 
     if (merge_here) {
         __syncthreads();
-        block_merge<G>(p, slot_item, slot_seg, wave, lane);
+        block_merge<G>(p, slot_item, part_lds, lse_lds, threadIdx.x);
     }
 }
 
