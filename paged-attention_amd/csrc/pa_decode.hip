@@ -174,42 +174,51 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, 
 // partial rows and base-2 LSEs, written to LDS by the wave that computed them.
 // Items appear in block order (wave, slot) as contiguous runs (ignoring empty
 // slots), and the planner turns this merge on only when every split row lies in
-// one block, so each run is a whole row. All threads of the block share the
-// outputs of a run (one head-dim element each): the base-2 LSE-weighted average
-// of the run's partials (decode_kernels.cuh:409-432), written as fp16.
+// one block, so each run is a whole row. Each thread owns one head-dim element
+// (two for G = 8) of every run: it reads that element of all 16 slots at once
+// (no LDS round trip per slot) and forms, per run, the base-2 LSE-weighted
+// average of the run's partials (decode_kernels.cuh:409-432), written as fp16.
 template <int G>
 __device__ __forceinline__ void block_merge(const pa_decode_params& p, const int (*slot_item)[2],
                                             const float (*part)[G * kHeadDim], const float (*lse)[G], int tid) {
     constexpr int NS = 2 * kWaves;
-    int i = 0;
-    while (i < NS) {
-        const int x = slot_item[i >> 1][i & 1];
-        if (x < 0) {
-            ++i;
-            continue;
+    constexpr int NO = G * kHeadDim;
+    static_assert(NS <= 64, "one lane per slot");
+    const int mine = slot_item[(tid & (NS - 1)) >> 1][tid & 1];
+    int item[NS];
+    unsigned starts = 0;   // slots that begin a run
+    int prev = -1;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+        item[s] = __builtin_amdgcn_readlane(mine, s);
+        if (item[s] >= 0 && item[s] != prev) starts |= 1u << s;
+        if (item[s] >= 0) prev = item[s];
+    }
+#pragma unroll
+    for (int o = tid; o < NO; o += 64 * kWaves) {
+        const int g = o / kHeadDim;
+        float lv[NS], pv[NS];
+#pragma unroll
+        for (int j = 0; j < NS; ++j) {
+            lv[j] = lse[j][g];
+            pv[j] = part[j][o];
         }
-        int j = i + 1;
-        for (; j < NS; ++j) {
-            const int it = slot_item[j >> 1][j & 1];
-            if (it >= 0 && it != x) break;
-        }
-        const int b = x / p.num_kv_heads, h = x - b * p.num_kv_heads;
-        uint16_t* orow = p.out + (static_cast<size_t>(b) * p.num_q_heads + h * G) * kHeadDim;
-        for (int o = tid; o < G * kHeadDim; o += 64 * kWaves) {
-            const int g = o / kHeadDim;
+        for (unsigned rs = starts; rs != 0; rs &= rs - 1) {
+            const int x = __builtin_amdgcn_readlane(mine, __builtin_ctz(rs));   // the run's item
             float mx = -INFINITY;
-            for (int s = i; s < j; ++s)
-                if (slot_item[s >> 1][s & 1] >= 0) mx = fmaxf(mx, lse[s][g]);
+#pragma unroll
+            for (int j = 0; j < NS; ++j) mx = item[j] == x ? fmaxf(mx, lv[j]) : mx;
             float a = 0.f, den = 0.f;
-            for (int s = i; s < j; ++s) {
-                if (slot_item[s >> 1][s & 1] < 0) continue;
-                const float w = exp2_fast(lse[s][g] - mx);
-                a = fmaf(w, part[s][o], a);
-                den += w;
+#pragma unroll
+            for (int j = 0; j < NS; ++j) {
+                const float w = exp2_fast(lv[j] - mx);
+                a   = item[j] == x ? fmaf(w, pv[j], a) : a;
+                den = item[j] == x ? den + w : den;
             }
-            orow[o] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(a * (1.0f / den)));
+            const int b = x / p.num_kv_heads, h = x - b * p.num_kv_heads;
+            p.out[(static_cast<size_t>(b) * p.num_q_heads + h * G) * kHeadDim + o] =
+                __builtin_bit_cast(uint16_t, static_cast<_Float16>(a * (1.0f / den)));
         }
-        i = j;
     }
 }
 
