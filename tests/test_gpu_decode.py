@@ -191,6 +191,50 @@ def test_block_merge_and_merge_kernel_agree(fp8):
         assert float(np.max(np.abs(o - ref))) < TOL
     assert float(np.max(np.abs(outs[0] - outs[1]))) < 1e-3
 
+@pytest.mark.parametrize("group", [1, 2, 4, 8])
+@pytest.mark.parametrize("fp8", DTYPES, ids=IDS)
+def test_block_merge_two_split_segments_per_unit(fp8, group):
+    """Items of 8 tiles over units of 3 tiles: each 8-unit block holds three
+    whole rows, and units 2 and 5 of a block end one row and start the next,
+    so those waves hold two split segments (both LDS slots) and a block merges
+    three runs of lengths 3, 4 and 3. Every group size (the LDS slot rows are
+    G x head_dim) must match the merge kernel on the same plan and the oracle."""
+    import torch
+    hkv = 8
+    hq = hkv * group
+    dt = pa_amd.FP8_E4M3 if fp8 else pa_amd.FP16
+    tile = pa_amd.tile_tokens(dt, D, group)
+    lens = [8 * tile] * 3                          # 24 items x 8 tiles = 192 tiles
+    units = 64                                     # 3 tiles per unit, 3 items per block
+    q, k, v, table, ks, vs = paged_inputs(len(lens), lens, hq, hkv, 16, fp8, seed=11 + group)
+    plan = pa_amd.make_plan(dt, lens, hq, hkv, D, units)
+    assert plan.num_ctas == units
+    dplan = pa_amd.DevicePlan()
+    dplan.upload(plan, group, D)
+    outs = []
+    for force_kernel in (False, True):
+        p = pa_amd.DecodeParams()
+        p.q, p.k_cache, p.v_cache, p.block_table = q.data_ptr(), k.data_ptr(), v.data_ptr(), table.data_ptr()
+        out = torch.empty_like(q)
+        p.out = out.data_ptr()
+        p.block_table_stride = table.size(1)
+        p.batch, p.num_q_heads, p.num_kv_heads, p.head_dim, p.page_size = len(lens), hq, hkv, D, 16
+        p.sm_scale, p.k_scale, p.v_scale = pa_amd.sm_scale(D), ks, vs
+        dplan.bind(p)
+        assert p.block_merge == 1 and p.needs_merge == 0
+        if force_kernel:
+            p.block_merge, p.needs_merge = 0, 1
+        pa_amd.paged_decode(dt, p)
+        torch.cuda.synchronize()
+        outs.append(out.float().cpu().numpy())
+    kb = k.view(torch.uint8).cpu().numpy() if fp8 else k.view(torch.int16).cpu().numpy().view(np.uint16)
+    vb = v.view(torch.uint8).cpu().numpy() if fp8 else v.view(torch.int16).cpu().numpy().view(np.uint16)
+    ref = oracle.paged_decode(dt, q.view(torch.int16).cpu().numpy().view(np.uint16), kb, vb, table.cpu().numpy(),
+                              np.asarray(lens, np.int32), hq, hkv, D, 16, ks, vs, threads=16)
+    for o in outs:
+        assert float(np.max(np.abs(o - ref))) < TOL
+    assert float(np.max(np.abs(outs[0] - outs[1]))) < 1e-3
+
 @pytest.mark.parametrize("lens", [[1024] * 4, [20000], [300, 4100, 17]], ids=["c1", "long", "ragged"])
 def test_graph_capture_replays_match_eager(lens):
     """A decode step (PagedKVCache::run: split + merge launches) captured into
