@@ -242,8 +242,18 @@ typedef struct pa_cache pa_cache;
 /* paged_kv_cache.cu:43-45 bytes_per_page; :47-49 pages_for_budget. */
 size_t    pa_cache_bytes_per_page(const pa_cache_config* cfg);
 int       pa_cache_pages_for_budget(const pa_cache_config* cfg, size_t budget_bytes);
-/* paged_kv_cache.cu:51-74 constructor (device pools, table, seq_lens). */
+/* paged_kv_cache.cu:51-74 constructor (device pools, table, seq_lens). The K
+ * and V pools share one allocation, V starting pa_kv_pool_stagger() bytes
+ * after the end of K. */
 pa_status pa_cache_create(const pa_cache_config* cfg, pa_cache** out);
+/* No counterpart in the reference: the byte gap this library leaves between
+ * the end of its K pool and the start of its V pool. A wave reads the same
+ * (page, kv head) run of both pools at once, and pools at the same offset
+ * modulo a large power of two put those reads on the same HBM banks (a decode
+ * step 3-7% slower on MI355X). Callers that allocate their own pools for
+ * pa_decode or the torch Decoder get the same placement by allocating both
+ * pools at once with V this many bytes after the end of K. */
+size_t    pa_kv_pool_stagger(void);
 void      pa_cache_destroy(pa_cache* cache);
 /* Host bookkeeping view (seq_len, free_pages, block tables, ...). */
 pa_pool*  pa_cache_pool(pa_cache* cache);

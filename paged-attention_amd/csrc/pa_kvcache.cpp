@@ -92,6 +92,7 @@ using namespace pa::host;
 extern "C" {
 
 size_t pa_cache_bytes_per_page(const pa_cache_config* cfg) { return cfg ? bytes_per_page_impl(*cfg) : 0; }
+size_t pa_kv_pool_stagger(void) { return pa::kPoolStagger; }
 
 int pa_cache_pages_for_budget(const pa_cache_config* cfg, size_t budget_bytes) {
     if (!cfg) return 0;
@@ -113,8 +114,10 @@ pa_status pa_cache_create(const pa_cache_config* cfg, pa_cache** out) {
             pool_init(c->pool, cfg->num_pages, cfg->page_size, cfg->max_slots, cfg->max_pages_per_slot);
             const size_t half_bytes = bytes_per_page_impl(*cfg) / 2 * static_cast<size_t>(cfg->num_pages);
             const size_t table = sizeof(int32_t) * static_cast<size_t>(cfg->max_slots) * cfg->max_pages_per_slot;
-            pa::hip_check(hipMalloc(&c->d_k, half_bytes), "hipMalloc k pool");
-            pa::hip_check(hipMalloc(&c->d_v, half_bytes), "hipMalloc v pool");
+            // One allocation for both pools, V starting kPoolStagger bytes after
+            // the end of K (the K/V bank-conflict gap).
+            pa::hip_check(hipMalloc(&c->d_k, 2 * half_bytes + pa::kPoolStagger), "hipMalloc k/v pools");
+            c->d_v = static_cast<unsigned char*>(c->d_k) + half_bytes + pa::kPoolStagger;
             pa::hip_check(hipMalloc(reinterpret_cast<void**>(&c->d_table), table), "hipMalloc block table");
             pa::hip_check(hipMalloc(reinterpret_cast<void**>(&c->d_seq_lens), sizeof(int32_t) * cfg->max_slots),
                           "hipMalloc seq_lens");
@@ -122,7 +125,6 @@ pa_status pa_cache_create(const pa_cache_config* cfg, pa_cache** out) {
             pa::hip_check(hipMemset(c->d_seq_lens, 0, sizeof(int32_t) * cfg->max_slots), "hipMemset");
         } catch (...) {
             (void)hipFree(c->d_k);
-            (void)hipFree(c->d_v);
             (void)hipFree(c->d_table);
             (void)hipFree(c->d_seq_lens);
             delete c;
@@ -134,8 +136,7 @@ pa_status pa_cache_create(const pa_cache_config* cfg, pa_cache** out) {
 
 void pa_cache_destroy(pa_cache* c) {
     if (!c) return;
-    (void)hipFree(c->d_k);
-    (void)hipFree(c->d_v);
+    (void)hipFree(c->d_k);   // both pools
     (void)hipFree(c->d_table);
     (void)hipFree(c->d_seq_lens);
     (void)hipFree(c->d_slot_ids);

@@ -10,7 +10,7 @@ from ._lib import DecodeParams, CacheConfig, PaError, InvalidArgument, LengthErr
 from .core import (FP16, FP8_E4M3, DecodePlan, DevicePlan, PagePool, PagedKVCache, make_plan,
                    make_plan_tiled, paged_decode, decode_split, decode_merge, append_quantize,
                    gather_kv, stream_read, stream_read_chunked, fill_bytes, tile_tokens, wave_ctas, default_ctas, kv_dtype_bytes,
-                   kv_dtype_name, sm_scale)
+                   kv_dtype_name, sm_scale, kv_pool_stagger, alloc_kv_pools)
 
 
 def Decoder(*args, **kwargs):
@@ -24,5 +24,5 @@ __all__ = [
     "DeviceError", "FP16", "FP8_E4M3", "DecodePlan", "DevicePlan", "PagePool", "PagedKVCache",
     "make_plan", "make_plan_tiled", "paged_decode", "decode_split", "decode_merge",
     "append_quantize", "gather_kv", "stream_read", "stream_read_chunked", "fill_bytes", "tile_tokens", "wave_ctas", "default_ctas",
-    "kv_dtype_bytes", "kv_dtype_name", "sm_scale", "Decoder",
+    "kv_dtype_bytes", "kv_dtype_name", "sm_scale", "kv_pool_stagger", "alloc_kv_pools", "Decoder",
 ]

@@ -144,6 +144,7 @@ SIGNATURES: dict[str, tuple] = {
     "pa_pool_num_pages_of": (_I, [_P, _I]),
     "pa_pool_block_table": (_I, [_P, _I, _P, _I]),
     "pa_cache_bytes_per_page": (_S, [ctypes.POINTER(CacheConfig)]),
+    "pa_kv_pool_stagger": (_S, []),
     "pa_cache_pages_for_budget": (_I, [ctypes.POINTER(CacheConfig), _S]),
     "pa_cache_create": (_I, [ctypes.POINTER(CacheConfig), _PP]),
     "pa_cache_destroy": (None, [_P]),

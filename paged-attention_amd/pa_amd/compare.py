@@ -61,6 +61,14 @@ def make_inputs(batch: int, seq_len: int, fp8: bool, seed: int = 0):
         v_scale = v.abs().max().item() / 448.0
         k = (k / k_scale).to(torch.float8_e4m3fn)
         v = (v / v_scale).to(torch.float8_e4m3fn)
+    # The same values in pools laid out as the library's own caches lay theirs
+    # out (one allocation, V a small gap after K; see core.alloc_kv_pools).
+    kp, vp = core.alloc_kv_pools(num_pages, HKV, PAGE, DIM, fp8)
+    if fp8:
+        kp, vp = kp.view(torch.float8_e4m3fn), vp.view(torch.float8_e4m3fn)
+    kp.copy_(k)
+    vp.copy_(v)
+    k, v = kp, vp
     perm = torch.randperm(num_pages, device="cuda", generator=g).to(torch.int32)
     block_table = perm.view(batch, pages_per_seq).contiguous()
     q = torch.randn(batch, HQ, DIM, device="cuda", dtype=torch.float16, generator=g)

@@ -77,3 +77,19 @@ def test_device_queries_report_errors_not_crashes():
     else:
         with pytest.raises(pa_amd.DeviceError):
             pa_amd.wave_ctas(pa_amd.FP16, 128, 4)
+
+
+def test_kv_pool_stagger_and_alloc_kv_pools():
+    """The library's K/V pool gap is a positive multiple of 4 KiB, and
+    alloc_kv_pools lays caller-owned pools out the same way: two views of one
+    allocation, V starting that many bytes after the end of K."""
+    import torch
+    gap = pa_amd.kv_pool_stagger()
+    assert gap > 0 and gap % 4096 == 0
+    for fp8, elem in ((False, 2), (True, 1)):
+        k, v = pa_amd.alloc_kv_pools(3, 2, 16, 128, fp8, device="cpu")
+        assert k.shape == v.shape == (3, 2, 16, 128)
+        assert k.dtype == (torch.uint8 if fp8 else torch.float16) == v.dtype
+        assert k.is_contiguous() and v.is_contiguous()
+        assert v.data_ptr() - k.data_ptr() == 3 * 2 * 16 * 128 * elem + gap
+        assert k.untyped_storage().data_ptr() == v.untyped_storage().data_ptr()
