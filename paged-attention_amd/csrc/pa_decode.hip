@@ -64,7 +64,7 @@
 #define PA_FP16_DEPTH 1
 #endif
 #ifndef PA_FP8_DEPTH
-#define PA_FP8_DEPTH 3
+#define PA_FP8_DEPTH 2
 #endif
 // 1: K/V loads are non-temporal (streamed once, kept out of the caches).
 #ifndef PA_FP16_NONTEMPORAL
@@ -91,6 +91,12 @@
 #ifndef PA_FP8_K_NATURAL
 #define PA_FP8_K_NATURAL 0
 #endif
+// FP8, page sizes that are powers of two >= 16: 1 = K and V are fetched with
+// fully coalesced 16-byte loads (each instruction 8 whole 128-byte rows) and
+// put into the MFMA lane layouts through an 8 KiB LDS stage per wave.
+#ifndef PA_FP8_LDS_STAGE
+#define PA_FP8_LDS_STAGE 1
+#endif
 
 namespace pa {
 namespace {
@@ -108,6 +114,7 @@ template <int EB> struct Tune {
     static constexpr int  depth = EB == 2 ? PA_FP16_DEPTH : PA_FP8_DEPTH;
     static constexpr bool nt    = EB == 2 ? PA_FP16_NONTEMPORAL != 0 : PA_FP8_NONTEMPORAL != 0;
     static constexpr bool knat  = EB == 2 ? PA_FP16_K_NATURAL != 0 : PA_FP8_K_NATURAL != 0;
+    static constexpr bool stage = EB == 1 && !knat && PA_FP8_LDS_STAGE != 0;
 };
 static_assert(Tune<2>::step == 16 || Tune<2>::step == 32, "fp16 step must be 16 or 32");
 static_assert(Tune<1>::step == 16 || Tune<1>::step == 32, "fp8 step must be 16 or 32");
@@ -243,11 +250,15 @@ __device__ __forceinline__ void decode_split_body(const pa_decode_params& p, int
     constexpr int  NQ    = G > 4 ? 2 : 1;           // compact Q registers per lane
     constexpr int  NVL   = PATH == kPageAny ? 4 : 1;   // V page lookups per lane (per-lane paths)
     constexpr int  HW    = G < 4 ? G : 4;           // live O rows per writing lane
+    constexpr bool STG   = Tune<EB>::stage && PATH == kPagePow2;   // K/V through the LDS stage
     using VRaw = std::conditional_t<EB == 2, u32x4, u32x2>;
     using KRaw = std::conditional_t<KL == 16, u32x4, u32x2>;
 
     __shared__ __attribute__((aligned(16))) u32x4 q_lds[kWaves][16 * G];   // G heads x 256 B per wave
     __shared__ int slot_item[kWaves][2];                                     // split segments per wave
+    // LDS stage of one step per wave (STG): [K, V][half][16 rows][128 B], each
+    // row's 16-byte chunks XOR-swizzled by (row % 8).
+    __shared__ __attribute__((aligned(16))) u32x4 stage_lds[STG ? kWaves : 1][STG ? 2 * NH * 128 : 1];
     // Partials of split segments for the block-level merge, slot 2 * wave + sl.
     __shared__ __attribute__((aligned(16))) float part_lds[2 * kWaves][G * kHeadDim];
     __shared__ float lse_lds[2 * kWaves][G];
@@ -284,6 +295,9 @@ __device__ __forceinline__ void decode_split_body(const pa_decode_params& p, int
     // ---- pipeline registers, indexed by ring slot = step index mod DEPTH
     KRaw  kr[DEPTH][NH][NK];   // K: token 16hh + c of each half
     VRaw  vr[DEPTH][NH][4];    // V: tokens 16hh + 4kb + r, dims 8c..8c+7
+    // LDS-staged FP8: the raw coalesced loads (rows 8 part + lane / 8, bytes
+    // 16 (lane % 8) .. +15 of each half), moved into kr / vr by the stage.
+    u32x4 kc[STG ? DEPTH : 1][NH][2], vc[STG ? DEPTH : 1][NH][2];
     u32x4 qc[DEPTH][NQ];       // compact Q, loaded with a segment's first step
     int   pg[DEPTH][NH];       // power-of-two path: page of each half (wave-uniform)
     int   pk[DEPTH][NH], sk[DEPTH][NH];            // per-lane paths: K token's page and slot
@@ -362,6 +376,16 @@ __device__ __forceinline__ void decode_split_body(const pa_decode_params& p, int
                                     static_cast<uint32_t>((L.h * P + (bt & (P - 1))) * ROW);
                 const __amdgpu_buffer_rsrc_t krs = buffer_rsrc(kbase + row0, nv * ROW);
                 const __amdgpu_buffer_rsrc_t vrs = buffer_rsrc(vbase + row0, nv * ROW);
+                if constexpr (STG) {
+#pragma unroll
+                    for (int part = 0; part < 2; ++part) {
+                        kc[s][hh][part] = __builtin_bit_cast(
+                            u32x4, __builtin_amdgcn_raw_buffer_load_b128(krs, 1024 * part + 16 * lane, 0, kAux<NT>));
+                        vc[s][hh][part] = __builtin_bit_cast(
+                            u32x4, __builtin_amdgcn_raw_buffer_load_b128(vrs, 1024 * part + 16 * lane, 0, kAux<NT>));
+                    }
+                    continue;
+                }
 #pragma unroll
                 for (int u = 0; u < NK; ++u) {
                     if constexpr (KL == 16)
@@ -506,6 +530,31 @@ __device__ __forceinline__ void decode_split_body(const pa_decode_params& p, int
             for (int j = 0; j < 4; ++j) qf[j] = ql[16 * hc + (KNAT ? 4 * j + kb : 4 * kb + j)];
             const int item = C.b * hkv + C.h;
             whole = p.item_seg_begin[item + 1] - p.item_seg_begin[item] == 1;
+        }
+        if constexpr (STG) {
+            // Coalesced rows -> LDS (16-byte chunk j of row r at chunk j ^ (r % 8))
+            // -> the K / V lane layouts of the direct loads.
+            u32x4* st = stage_lds[wave];
+            const int wrow = lane >> 3;   // row within a 1 KiB part (row % 8)
+#pragma unroll
+            for (int hh = 0; hh < NH; ++hh)
+#pragma unroll
+                for (int part = 0; part < 2; ++part) {
+                    const int slot = 8 * (8 * part + wrow) + ((lane & 7) ^ wrow);
+                    st[hh * 128 + slot]        = kc[s][hh][part];
+                    st[(NH + hh) * 128 + slot] = vc[s][hh][part];
+                }
+#pragma unroll
+            for (int hh = 0; hh < NH; ++hh) {
+#pragma unroll
+                for (int u = 0; u < 2; ++u) kr[s][hh][u] = st[hh * 128 + 8 * c + ((2 * kb + u) ^ (c & 7))];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int row = 4 * kb + r;
+                    const u32x2* vrow = reinterpret_cast<const u32x2*>(st + (NH + hh) * 128 + 8 * row);
+                    vr[s][hh][r] = vrow[2 * ((c >> 1) ^ (row & 7)) + (c & 1)];
+                }
+            }
         }
         // S^T[token][head] per 16-token half; lane (c, kb) gets tokens 4kb+i.
         float x[NH][4];
