@@ -8,16 +8,23 @@
 //     segments in steps of NG = 16 or 32 tokens (two 16-token halves), DEPTH
 //     steps of K/V in flight in registers. The pages of a step are looked up
 //     another DEPTH steps ahead, so an HBM load never waits on the block table.
-//   * K is fetched token-major: in each 16-token half, lane (c, kb) holds
-//     token c and a quarter of its dims. That is the A-operand layout of
+//   * K is held token-major: in each 16-token half, lane (c, kb) holds token
+//     c and a quarter of its dims. That is the A-operand layout of
 //     v_mfma_f32_16x16x32_f16 for S^T = K Q^T with the G query heads sharing
-//     the kv head as B columns, so K never goes through LDS.
-//   * V is fetched dim-major: lane (c, kb) holds tokens 4kb..4kb+3 of each
-//     half, dims 8c..8c+7. After a v_perm regroup that is the B operand of the
-//     P V MFMA (MFMA j <-> dims 8c + j): 16x16x16 for 16-token steps, 16x16x32
+//     the kv head as B columns.
+//   * V is held dim-major: lane (c, kb) holds tokens 4kb..4kb+3 of each half,
+//     dims 8c..8c+7. After a v_perm regroup that is the B operand of the P V
+//     MFMA (MFMA j <-> dims 8c + j): 16x16x16 for 16-token steps, 16x16x32
 //     with the two halves as one k-block for 32-token steps. The S^T
 //     accumulators are already the A-operand layout of P, so P never leaves
 //     registers.
+//   * fp16 loads K and V straight into those layouts. FP8 rows are 128 B, so
+//     the same layouts would split every row over many lanes' small pieces;
+//     the FP8 kernel instead loads each 16-token half fully coalesced (16 B
+//     per lane, 8 whole rows per instruction) and moves it into the layouts
+//     through a per-wave LDS stage whose 16-byte chunks are XOR-swizzled by
+//     row, so both the row-wise writes and the column-wise K reads are free
+//     of bank conflicts.
 //   * When the page size is a power of two >= 16, a 16-token half lies in one
 //     page: one wave-uniform scalar lookup per half, and each load is a raw
 //     buffer load from an SGPR resource based at the half's first row, with
@@ -36,12 +43,13 @@
 //   * Q of each segment is fetched compactly (G x 256 B across the wave) with
 //     the segment's first K/V loads and expanded to the B-operand layout
 //     through a per-wave LDS slot once per segment.
-//   * When every split row lies inside one block of 8 work units (as at
-//     C2 / C3 shapes) the rows are merged in the block and no merge launch is
-//     needed: a unit's split segments are only its first and last, so each
-//     wave records at most two in LDS; after one barrier the wave that holds a
-//     row's first split segment combines the row's partials (written by waves
-//     of the same CU, so visible after the workgroup barrier) into the output.
+//   * When every split row lies inside one block of 8 work units (e.g. 32
+//     rows x 8 kv heads x 8192 tokens over 2048 units) the rows are merged in
+//     the block and no merge launch is needed: a unit's split segments are
+//     only its first and last, so each wave keeps at most two partials (and
+//     their LSEs) in LDS; after one barrier every thread of the block merges
+//     one head-dim element of each split row into the output. Otherwise the
+//     partials go to the plan's HBM workspace for the merge kernel.
 
 #include "pa_device.hpp"
 
@@ -725,7 +733,8 @@ void decode_split_kernel_fp8(const pa_decode_params p, int page_shift) {
 // ---------------------------------------------------------------------------
 // Merge (decode_kernels.cuh:409-432): one block per (query head, batch row,
 // DS-dim slice) of a row split over n > 1 segments; slicing the 128 dims over
-// 128 / DS blocks spreads a few long rows (C5: 32 rows of 256 segments) over
+// 128 / DS blocks spreads a few long rows (one 131072-token sequence: 32
+// (query head, row) pairs of 256 segments) over
 // every CU, since one CU streams only ~25 GB/s. DS / 4 lanes cover a segment's
 // slice (4 dims each, one 16-byte load), so a wave covers 256 / DS segments at
 // a time. A single pass over the segments with a running base-2 maximum per
@@ -860,8 +869,9 @@ hipError_t launch_split_e(const pa_decode_params& p, int group, hipStream_t s) {
     throw std::invalid_argument("unsupported GQA group size " + std::to_string(group));
 }
 
-// About four segments per lane measured best (C1: 64 segments per row, one
-// wave; C5: 256, four waves); sixteen waves per block cost ~1 us more at C5.
+// About four segments per lane measured best (4 x 1024 tokens: 64 segments
+// per row, one wave; 1 x 131072: 256, four waves); sixteen waves per block
+// cost ~1 us more at 1 x 131072.
 template <int G, int DS>
 hipError_t launch_merge_gd(const pa_decode_params& p, hipStream_t s) {
     const dim3 grid(p.num_q_heads, p.batch, kHeadDim / DS);
