@@ -132,6 +132,8 @@ enum PagePath : int {
     kPagePow2 = 0,   // page_size a power of two >= 16: a 16-token half is in one page
     kPageQuad = 1,   // page_size 4 or 8: one lookup per lane for K and one for V
     kPageAny  = 2,   // any other page size: one lookup per token, integer division
+    kPageRun8 = 3,   // FP8 with the LDS stage, page_size 8: one wave-uniform page per
+                     // 8-token part of a half (the rows of one coalesced load)
 };
 
 // One position of a wave's schedule: the current step of the current segment.
@@ -258,7 +260,7 @@ __device__ __forceinline__ void decode_split_body(const pa_decode_params& p, int
     constexpr int  NQ    = G > 4 ? 2 : 1;           // compact Q registers per lane
     constexpr int  NVL   = PATH == kPageAny ? 4 : 1;   // V page lookups per lane (per-lane paths)
     constexpr int  HW    = G < 4 ? G : 4;           // live O rows per writing lane
-    constexpr bool STG   = Tune<EB>::stage && PATH == kPagePow2;   // K/V through the LDS stage
+    constexpr bool STG   = Tune<EB>::stage && (PATH == kPagePow2 || PATH == kPageRun8);   // K/V via LDS
     using VRaw = std::conditional_t<EB == 2, u32x4, u32x2>;
     using KRaw = std::conditional_t<KL == 16, u32x4, u32x2>;
 
@@ -308,6 +310,7 @@ __device__ __forceinline__ void decode_split_body(const pa_decode_params& p, int
     u32x4 kc[STG ? DEPTH : 1][NH][2], vc[STG ? DEPTH : 1][NH][2];
     u32x4 qc[DEPTH][NQ];       // compact Q, loaded with a segment's first step
     int   pg[DEPTH][NH];       // power-of-two path: page of each half (wave-uniform)
+    int   pg8[PATH == kPageRun8 ? DEPTH : 1][NH][2];   // 8-token pages: page of each part
     int   pk[DEPTH][NH], sk[DEPTH][NH];            // per-lane paths: K token's page and slot
     int   pv[DEPTH][NH][NVL], sv[DEPTH][NH][NVL];  // per-lane paths: V tokens' page(s) and slot(s)
 
@@ -325,6 +328,14 @@ __device__ __forceinline__ void decode_split_body(const pa_decode_params& p, int
             if (t_more) {
 #pragma unroll
                 for (int hh = 0; hh < NH; ++hh) pg[s][hh] = t_row[min(T.tok + 16 * hh, T.w - 1) >> page_shift];
+            }
+        } else if constexpr (PATH == kPageRun8) {
+            if (t_more) {
+#pragma unroll
+                for (int hh = 0; hh < NH; ++hh)
+#pragma unroll
+                    for (int part = 0; part < 2; ++part)
+                        pg8[s][hh][part] = t_row[min(T.tok + 16 * hh + 8 * part, T.w - 1) >> page_shift];
             }
         } else {
             // Per-lane lookups repeat T's last step once it is exhausted, so
@@ -413,6 +424,24 @@ __device__ __forceinline__ void decode_split_body(const pa_decode_params& p, int
                             u32x2, __builtin_amdgcn_raw_buffer_load_b64(vrs, v_lane_off + r * ROW, 0, kAux<NT>));
                 }
             }
+        } else if constexpr (PATH == kPageRun8) {
+#pragma unroll
+            for (int hh = 0; hh < NH; ++hh)
+#pragma unroll
+                for (int part = 0; part < 2; ++part) {
+                    const int t  = L.tok + 16 * hh + 8 * part;   // first token of the part (a page start)
+                    const int bt = min(t, L.w - 1);
+                    const int nv = __builtin_amdgcn_readfirstlane(l_more ? max(0, min(8, L.w - t)) : 0);
+                    const size_t row0 =
+                        static_cast<size_t>(__builtin_amdgcn_readfirstlane(pg8[s][hh][part])) * page_bytes +
+                        static_cast<uint32_t>((L.h * P + (bt & (P - 1))) * ROW);
+                    const __amdgpu_buffer_rsrc_t krs = buffer_rsrc(kbase + row0, nv * ROW);
+                    const __amdgpu_buffer_rsrc_t vrs = buffer_rsrc(vbase + row0, nv * ROW);
+                    kc[s][hh][part] = __builtin_bit_cast(
+                        u32x4, __builtin_amdgcn_raw_buffer_load_b128(krs, 16 * lane, 0, kAux<NT>));
+                    vc[s][hh][part] = __builtin_bit_cast(
+                        u32x4, __builtin_amdgcn_raw_buffer_load_b128(vrs, 16 * lane, 0, kAux<NT>));
+                }
         } else {
 #pragma unroll
             for (int hh = 0; hh < NH; ++hh) {
@@ -829,7 +858,13 @@ __global__ __launch_bounds__(64 * WAVES) void decode_merge_kernel(const pa_decod
 
 // Steps in flight on the per-lane page paths (they keep the power-of-two
 // path's step, so results do not depend on the page size).
-template <int EB> constexpr int kLaneDepth = Tune<EB>::step == 16 ? 3 : 2;
+#ifndef PA_FP16_LANE_DEPTH
+#define PA_FP16_LANE_DEPTH 1
+#endif
+#ifndef PA_FP8_LANE_DEPTH
+#define PA_FP8_LANE_DEPTH 2
+#endif
+template <int EB> constexpr int kLaneDepth = EB == 2 ? PA_FP16_LANE_DEPTH : PA_FP8_LANE_DEPTH;
 
 template <int EB, int G, int NG, int DEPTH, int PATH>
 hipError_t launch_split_p(const pa_decode_params& p, int shift, hipStream_t s) {
@@ -853,6 +888,13 @@ hipError_t launch_split_g(const pa_decode_params& p, hipStream_t s) {
         if (static_cast<long long>(p.num_kv_heads) * P * kRowBytes<EB> >= (1ll << 31))
             throw std::invalid_argument("decode: page_size * num_kv_heads * row bytes must be below 2^31");
         return launch_split_p<EB, G, Tune<EB>::step, Tune<EB>::depth, kPagePow2>(p, shift, s);
+    }
+    if constexpr (Tune<EB>::stage) {
+        if (P == 8) {
+            if (static_cast<long long>(p.num_kv_heads) * P * kRowBytes<EB> >= (1ll << 31))
+                throw std::invalid_argument("decode: page_size * num_kv_heads * row bytes must be below 2^31");
+            return launch_split_p<EB, G, Tune<EB>::step, Tune<EB>::depth, kPageRun8>(p, shift, s);
+        }
     }
     if (pow2 && P >= 4) return launch_split_p<EB, G, Tune<EB>::step, kLaneDepth<EB>, kPageQuad>(p, shift, s);
     return launch_split_p<EB, G, Tune<EB>::step, kLaneDepth<EB>, kPageAny>(p, shift, s);

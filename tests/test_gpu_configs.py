@@ -94,6 +94,25 @@ def test_full_size_output_invariant_under_page_placement():
         del k, v, kp, vp
     assert np.array_equal(outs[0], outs[1])
 
+@pytest.mark.parametrize("fp8", DTYPES, ids=IDS)
+def test_alloc_kv_pools_decode_bitwise_equal(fp8):
+    """Pools laid out by alloc_kv_pools (one allocation, V a gap after K) hold
+    the same pages as separately allocated pools and decode bitwise equal."""
+    import torch
+    lens = [3000, 1, 777, 4096]
+    q, k, v, table, ks, vs = paged_inputs(len(lens), lens, 32, 8, 16, fp8, seed=21)
+    kp, vp = pa_amd.alloc_kv_pools(k.shape[0], 8, 16, D, fp8)
+    assert vp.data_ptr() - kp.data_ptr() == k.numel() * k.element_size() + pa_amd.kv_pool_stagger()
+    kp.copy_(k.view(kp.dtype))
+    vp.copy_(v.view(vp.dtype))
+    dec = pa_amd.Decoder(32, 8, D, 16, fp8)
+    t = torch.tensor(lens, dtype=torch.int32)
+    dec.plan(t, 0)
+    a = dec.run(q, k, v, table, t.cuda(), ks, vs)
+    b = dec.run(q, kp, vp, table, t.cuda(), ks, vs)
+    torch.cuda.synchronize()
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
 def test_decoder_rejects_inconsistent_inputs():
     """Decoder.run raises RuntimeError (the reference's TORCH_CHECK) for inputs
     whose shapes or types do not match the plan, before any launch."""

@@ -74,7 +74,7 @@ def test_output_invariant_under_page_placement(fp8):
     must be bitwise identical across page permutations and page sizes."""
     lens = [700, 1, 2049, 64]
     outs = []
-    for page_size, shuffle in [(16, None), (16, 3), (4, 11), (1, 5), (2048 + 64, None)]:
+    for page_size, shuffle in [(16, None), (16, 3), (8, 2), (4, 11), (1, 5), (2048 + 64, None)]:
         _, out, _ = run_cache_case(fp8, 32, 8, page_size, lens, shuffle_seed=shuffle)
         outs.append(out)
     for o in outs[1:]:
