@@ -132,8 +132,8 @@ enum PagePath : int {
     kPagePow2 = 0,   // page_size a power of two >= 16: a 16-token half is in one page
     kPageQuad = 1,   // page_size 4 or 8: one lookup per lane for K and one for V
     kPageAny  = 2,   // any other page size: one lookup per token, integer division
-    kPageRun8 = 3,   // FP8 with the LDS stage, page_size 8: one wave-uniform page per
-                     // 8-token part of a half (the rows of one coalesced load)
+    kPageRuns = 3,   // page_size 4 or 8 (fp16) / 8 (FP8 with the LDS stage): K/V through
+                     // the LDS stage, one wave-uniform page per coalesced 1 KiB part
 };
 
 // One position of a wave's schedule: the current step of the current segment.
@@ -260,15 +260,19 @@ __device__ __forceinline__ void decode_split_body(const pa_decode_params& p, int
     constexpr int  NQ    = G > 4 ? 2 : 1;           // compact Q registers per lane
     constexpr int  NVL   = PATH == kPageAny ? 4 : 1;   // V page lookups per lane (per-lane paths)
     constexpr int  HW    = G < 4 ? G : 4;           // live O rows per writing lane
-    constexpr bool STG   = Tune<EB>::stage && (PATH == kPagePow2 || PATH == kPageRun8);   // K/V via LDS
+    constexpr bool STG   = PATH == kPageRuns || (Tune<EB>::stage && PATH == kPagePow2);   // K/V via LDS
+    constexpr int  RPP   = 1024 / ROW;              // rows per coalesced 1 KiB part (4 fp16, 8 FP8)
+    constexpr int  NPART = 16 / RPP;                // parts per 16-token half
+    constexpr int  CPR   = ROW / 16;                // 16-byte chunks per row
+    constexpr int  HCH   = 16 * CPR;                // 16-byte chunks per half (256 B per row x 16)
     using VRaw = std::conditional_t<EB == 2, u32x4, u32x2>;
     using KRaw = std::conditional_t<KL == 16, u32x4, u32x2>;
 
     __shared__ __attribute__((aligned(16))) u32x4 q_lds[kWaves][16 * G];   // G heads x 256 B per wave
     __shared__ int slot_item[kWaves][2];                                     // split segments per wave
-    // LDS stage of one step per wave (STG): [K, V][half][16 rows][128 B], each
-    // row's 16-byte chunks XOR-swizzled by (row % 8).
-    __shared__ __attribute__((aligned(16))) u32x4 stage_lds[STG ? kWaves : 1][STG ? 2 * NH * 128 : 1];
+    // LDS stage of one step per wave (STG): [K, V][half][16 rows][row bytes],
+    // each row's 16-byte chunks XOR-swizzled by (row % chunks per row).
+    __shared__ __attribute__((aligned(16))) u32x4 stage_lds[STG ? kWaves : 1][STG ? 2 * NH * HCH : 1];
     // Partials of split segments for the block-level merge, slot 2 * wave + sl.
     __shared__ __attribute__((aligned(16))) float part_lds[2 * kWaves][G * kHeadDim];
     __shared__ float lse_lds[2 * kWaves][G];
@@ -307,10 +311,10 @@ __device__ __forceinline__ void decode_split_body(const pa_decode_params& p, int
     VRaw  vr[DEPTH][NH][4];    // V: tokens 16hh + 4kb + r, dims 8c..8c+7
     // LDS-staged FP8: the raw coalesced loads (rows 8 part + lane / 8, bytes
     // 16 (lane % 8) .. +15 of each half), moved into kr / vr by the stage.
-    u32x4 kc[STG ? DEPTH : 1][NH][2], vc[STG ? DEPTH : 1][NH][2];
+    u32x4 kc[STG ? DEPTH : 1][NH][NPART], vc[STG ? DEPTH : 1][NH][NPART];
     u32x4 qc[DEPTH][NQ];       // compact Q, loaded with a segment's first step
     int   pg[DEPTH][NH];       // power-of-two path: page of each half (wave-uniform)
-    int   pg8[PATH == kPageRun8 ? DEPTH : 1][NH][2];   // 8-token pages: page of each part
+    int   pgr[PATH == kPageRuns ? DEPTH : 1][NH][NPART];   // small pages: page of each part
     int   pk[DEPTH][NH], sk[DEPTH][NH];            // per-lane paths: K token's page and slot
     int   pv[DEPTH][NH][NVL], sv[DEPTH][NH][NVL];  // per-lane paths: V tokens' page(s) and slot(s)
 
@@ -329,13 +333,13 @@ __device__ __forceinline__ void decode_split_body(const pa_decode_params& p, int
 #pragma unroll
                 for (int hh = 0; hh < NH; ++hh) pg[s][hh] = t_row[min(T.tok + 16 * hh, T.w - 1) >> page_shift];
             }
-        } else if constexpr (PATH == kPageRun8) {
+        } else if constexpr (PATH == kPageRuns) {
             if (t_more) {
 #pragma unroll
                 for (int hh = 0; hh < NH; ++hh)
 #pragma unroll
-                    for (int part = 0; part < 2; ++part)
-                        pg8[s][hh][part] = t_row[min(T.tok + 16 * hh + 8 * part, T.w - 1) >> page_shift];
+                    for (int part = 0; part < NPART; ++part)
+                        pgr[s][hh][part] = t_row[min(T.tok + 16 * hh + RPP * part, T.w - 1) >> page_shift];
             }
         } else {
             // Per-lane lookups repeat T's last step once it is exhausted, so
@@ -397,7 +401,7 @@ __device__ __forceinline__ void decode_split_body(const pa_decode_params& p, int
                 const __amdgpu_buffer_rsrc_t vrs = buffer_rsrc(vbase + row0, nv * ROW);
                 if constexpr (STG) {
 #pragma unroll
-                    for (int part = 0; part < 2; ++part) {
+                    for (int part = 0; part < NPART; ++part) {
                         kc[s][hh][part] = __builtin_bit_cast(
                             u32x4, __builtin_amdgcn_raw_buffer_load_b128(krs, 1024 * part + 16 * lane, 0, kAux<NT>));
                         vc[s][hh][part] = __builtin_bit_cast(
@@ -424,16 +428,16 @@ __device__ __forceinline__ void decode_split_body(const pa_decode_params& p, int
                             u32x2, __builtin_amdgcn_raw_buffer_load_b64(vrs, v_lane_off + r * ROW, 0, kAux<NT>));
                 }
             }
-        } else if constexpr (PATH == kPageRun8) {
+        } else if constexpr (PATH == kPageRuns) {
 #pragma unroll
             for (int hh = 0; hh < NH; ++hh)
 #pragma unroll
-                for (int part = 0; part < 2; ++part) {
-                    const int t  = L.tok + 16 * hh + 8 * part;   // first token of the part (a page start)
+                for (int part = 0; part < NPART; ++part) {
+                    const int t  = L.tok + 16 * hh + RPP * part;   // first token of the part (inside one page)
                     const int bt = min(t, L.w - 1);
-                    const int nv = __builtin_amdgcn_readfirstlane(l_more ? max(0, min(8, L.w - t)) : 0);
+                    const int nv = __builtin_amdgcn_readfirstlane(l_more ? max(0, min(RPP, L.w - t)) : 0);
                     const size_t row0 =
-                        static_cast<size_t>(__builtin_amdgcn_readfirstlane(pg8[s][hh][part])) * page_bytes +
+                        static_cast<size_t>(__builtin_amdgcn_readfirstlane(pgr[s][hh][part])) * page_bytes +
                         static_cast<uint32_t>((L.h * P + (bt & (P - 1))) * ROW);
                     const __amdgpu_buffer_rsrc_t krs = buffer_rsrc(kbase + row0, nv * ROW);
                     const __amdgpu_buffer_rsrc_t vrs = buffer_rsrc(vbase + row0, nv * ROW);
@@ -569,27 +573,35 @@ __device__ __forceinline__ void decode_split_body(const pa_decode_params& p, int
             whole = p.item_seg_begin[item + 1] - p.item_seg_begin[item] == 1;
         }
         if constexpr (STG) {
-            // Coalesced rows -> LDS (16-byte chunk j of row r at chunk j ^ (r % 8))
+            // Coalesced rows -> LDS (16-byte chunk j of row r at chunk j ^ (r % CPR))
             // -> the K / V lane layouts of the direct loads.
             u32x4* st = stage_lds[wave];
-            const int wrow = lane >> 3;   // row within a 1 KiB part (row % 8)
+            const int wrow = lane / CPR;   // row within a 1 KiB part
 #pragma unroll
             for (int hh = 0; hh < NH; ++hh)
 #pragma unroll
-                for (int part = 0; part < 2; ++part) {
-                    const int slot = 8 * (8 * part + wrow) + ((lane & 7) ^ wrow);
-                    st[hh * 128 + slot]        = kc[s][hh][part];
-                    st[(NH + hh) * 128 + slot] = vc[s][hh][part];
+                for (int part = 0; part < NPART; ++part) {
+                    const int row  = RPP * part + wrow;
+                    const int slot = CPR * row + ((lane % CPR) ^ (row % CPR));
+                    st[hh * HCH + slot]        = kc[s][hh][part];
+                    st[(NH + hh) * HCH + slot] = vc[s][hh][part];
                 }
 #pragma unroll
             for (int hh = 0; hh < NH; ++hh) {
 #pragma unroll
-                for (int u = 0; u < 2; ++u) kr[s][hh][u] = st[hh * 128 + 8 * c + ((2 * kb + u) ^ (c & 7))];
+                for (int u = 0; u < NK; ++u) {
+                    const int ch = (kb * KLANE + KSTEP * u) / 16;   // chunk of row c this load holds
+                    kr[s][hh][u] = st[hh * HCH + CPR * c + (ch ^ (c % CPR))];
+                }
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const int row = 4 * kb + r;
-                    const u32x2* vrow = reinterpret_cast<const u32x2*>(st + (NH + hh) * 128 + 8 * row);
-                    vr[s][hh][r] = vrow[2 * ((c >> 1) ^ (row & 7)) + (c & 1)];
+                    const u32x4* vrow = st + (NH + hh) * HCH + CPR * row;
+                    if constexpr (EB == 2) {
+                        vr[s][hh][r] = vrow[c ^ (row % CPR)];
+                    } else {
+                        vr[s][hh][r] = reinterpret_cast<const u32x2*>(vrow)[2 * ((c >> 1) ^ (row % CPR)) + (c & 1)];
+                    }
                 }
             }
         }
@@ -889,11 +901,12 @@ hipError_t launch_split_g(const pa_decode_params& p, hipStream_t s) {
             throw std::invalid_argument("decode: page_size * num_kv_heads * row bytes must be below 2^31");
         return launch_split_p<EB, G, Tune<EB>::step, Tune<EB>::depth, kPagePow2>(p, shift, s);
     }
-    if constexpr (Tune<EB>::stage) {
-        if (P == 8) {
+    // Pages of whole 1 KiB parts (4 fp16 rows, 8 FP8 rows) through the LDS stage.
+    if (P == 8 || (EB == 2 && P == 4)) {
+        if constexpr (EB == 2 || Tune<EB>::stage) {
             if (static_cast<long long>(p.num_kv_heads) * P * kRowBytes<EB> >= (1ll << 31))
                 throw std::invalid_argument("decode: page_size * num_kv_heads * row bytes must be below 2^31");
-            return launch_split_p<EB, G, Tune<EB>::step, Tune<EB>::depth, kPageRun8>(p, shift, s);
+            return launch_split_p<EB, G, Tune<EB>::step, Tune<EB>::depth, kPageRuns>(p, shift, s);
         }
     }
     if (pow2 && P >= 4) return launch_split_p<EB, G, Tune<EB>::step, kLaneDepth<EB>, kPageQuad>(p, shift, s);
