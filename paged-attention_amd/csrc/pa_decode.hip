@@ -105,6 +105,10 @@
 #ifndef PA_FP8_LDS_STAGE
 #define PA_FP8_LDS_STAGE 1
 #endif
+// The same for fp16 pages of 16 tokens and more (4 rows per 1 KiB load).
+#ifndef PA_FP16_LDS_STAGE
+#define PA_FP16_LDS_STAGE 0
+#endif
 
 namespace pa {
 namespace {
@@ -122,7 +126,7 @@ template <int EB> struct Tune {
     static constexpr int  depth = EB == 2 ? PA_FP16_DEPTH : PA_FP8_DEPTH;
     static constexpr bool nt    = EB == 2 ? PA_FP16_NONTEMPORAL != 0 : PA_FP8_NONTEMPORAL != 0;
     static constexpr bool knat  = EB == 2 ? PA_FP16_K_NATURAL != 0 : PA_FP8_K_NATURAL != 0;
-    static constexpr bool stage = EB == 1 && !knat && PA_FP8_LDS_STAGE != 0;
+    static constexpr bool stage = EB == 2 ? PA_FP16_LDS_STAGE != 0 : !knat && PA_FP8_LDS_STAGE != 0;
 };
 static_assert(Tune<2>::step == 16 || Tune<2>::step == 32, "fp16 step must be 16 or 32");
 static_assert(Tune<1>::step == 16 || Tune<1>::step == 32, "fp8 step must be 16 or 32");
