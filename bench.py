@@ -46,6 +46,7 @@ import json
 import os
 import pathlib
 import statistics
+import subprocess
 import sys
 import time
 
@@ -207,7 +208,6 @@ def measure_traffic(args) -> dict | None:
     or None if the profiler is unavailable or a pass fails."""
     import csv
     import shutil
-    import subprocess
     import tempfile
     prof = shutil.which("rocprofv3")
     if not prof:
@@ -244,6 +244,22 @@ def measure_traffic(args) -> dict | None:
     return out
 
 
+def device_report() -> dict:
+    """The box's own figures for the GPU (`amd-smi static`), so the line carries
+    the reported HBM bandwidth beside the published 8 TB/s it is priced against.
+    Runs as a child process before this process touches the GPU."""
+    try:
+        proc = subprocess.run(["amd-smi", "static", "--gpu", "0", "--json"], capture_output=True, text=True,
+                              timeout=60)
+        g = json.loads(proc.stdout)["gpu_data"][0]
+        vram, asic = g["vram"], g["asic"]
+        return {"name": asic.get("market_name"), "arch": asic.get("target_graphics_version"),
+                "cus": asic.get("num_compute_units"), "hbm": f"{vram.get('type')} {vram['size']['value']} MB",
+                "reported_max_bandwidth_gbps": vram["max_bandwidth"]["value"], "source": "amd-smi static"}
+    except (OSError, ValueError, KeyError, IndexError, TypeError, subprocess.SubprocessError) as e:
+        return {"source": f"amd-smi unavailable ({type(e).__name__})"}
+
+
 def _barrier() -> None:
     import torch.distributed as dist
     if dist.is_available() and dist.is_initialized():
@@ -277,8 +293,10 @@ def main() -> None:
               file=sys.stderr)
         sys.exit(2)
 
-    # The counter passes run before this process initializes the GPU.
+    # The counter passes and the device query run before this process
+    # initializes the GPU.
     traffic = None if args.no_traffic else measure_traffic(args)
+    device = device_report()
 
     import torch
     if not torch.cuda.is_available():
@@ -385,6 +403,7 @@ def main() -> None:
         threads = args.cpu_threads or min(16, os.cpu_count() or 1)
         result["cpu_baseline"] = cpu_baseline(s, args.config, args.cpu_budget, threads)
 
+    result["device"] = device
     s.close()
     print(json.dumps(result), flush=True)
 

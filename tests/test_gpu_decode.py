@@ -41,7 +41,7 @@ def test_mixed_length_batch(fp8):
     assert err < TOL, err
 
 @pytest.mark.parametrize("fp8", DTYPES, ids=IDS)
-@pytest.mark.parametrize("page_size", [1, 3, 8, 16, 32, 128])
+@pytest.mark.parametrize("page_size", [1, 3, 4, 8, 16, 32, 128])
 def test_page_sizes(fp8, page_size):
     err, _, _ = run_cache_case(fp8, 16, 4, page_size, [300, 2500])
     assert err < TOL, err
@@ -88,7 +88,7 @@ def test_seeded_random_configurations(case):
     rng = np.random.default_rng(1000 + case)
     fp8 = bool(rng.integers(0, 2))
     hq, hkv = [(8, 8), (8, 4), (16, 4), (32, 8), (8, 1), (32, 4)][int(rng.integers(0, 6))]
-    page = int(rng.choice([1, 2, 3, 5, 8, 16, 32, 64, 128]))
+    page = int(rng.choice([1, 2, 3, 4, 5, 8, 16, 32, 64, 128]))
     lens = [int(x) for x in rng.integers(1, 3001, size=int(rng.integers(1, 9)))]
     ctas = int(rng.choice([0, 0, 1, 3, 17, 300]))
     chunk = int(rng.choice([0, 0, 7, 64]))
