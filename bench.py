@@ -391,6 +391,11 @@ def main() -> None:
         result["copy_ceiling"] = {
             "gbps": round(best["gbps"], 1), "frac": round(best["gbps"] / PEAK_GBPS, 4), "kernel": best["kernel"],
             "reference_read_gbps": round(max(r["gbps"] for r in ref_rows), 1), "bytes": best["bytes"]}
+        same = bd.chunked_read_same_bytes(cus, nbytes)
+        if same:
+            result["copy_ceiling"]["same_size"] = {
+                "bytes": same["bytes"], "gbps": round(same["gbps"], 1), "frac": round(same["gbps"] / PEAK_GBPS, 4),
+                "kernel": same["kernel"], "time_us": round(same["time_us"], 2)}
     if not args.no_cold:
         fl = bd.Flusher()
         cold = bd.time_cold(fl, args.cold_iters, s.run)

@@ -208,6 +208,44 @@ def copy_rows(cus: int, iters: int = 10, nbytes: int = 4 << 30) -> list[dict]:
     return rows
 
 
+def chunked_read_same_bytes(cus: int, nbytes: int, iters: int = 10) -> dict | None:
+    """The best chunked streaming read (one contiguous span per wave) of about
+    `nbytes` (rounded down to what the span shapes divide): the read ceiling at
+    a workload's own size, where launch ramp and tail weigh as they do for it."""
+    import torch
+    best = None
+    for mult, unroll in ((1, 16), (2, 16), (4, 8)):
+        blocks = cus * mult
+        gran = blocks * 8 * unroll * 1024          # waves x unroll x 1 KiB
+        n = nbytes // gran * gran
+        if n == 0:
+            continue
+        buf = torch.ones(n, dtype=torch.uint8, device="cuda")
+        sink = torch.zeros(1, dtype=torch.int32, device="cuda")
+        stream = torch.cuda.current_stream()
+        ms = []
+        try:
+            for i in range(iters + 2):
+                a = torch.cuda.Event(enable_timing=True)
+                b = torch.cuda.Event(enable_timing=True)
+                a.record(stream)
+                core.stream_read_chunked(buf, n, blocks, sink, stream, threads=512, unroll=unroll)
+                b.record(stream)
+                b.synchronize()
+                if i >= 2:
+                    ms.append(a.elapsed_time(b))
+        except InvalidArgument:
+            continue
+        finally:
+            del buf
+        med = statistics.median(ms)
+        row = {"kernel": f"read_chunked_{blocks}x512_u{unroll}_nt", "bytes": n, "time_us": med * 1e3,
+               "gbps": n / (med * 1e-3) / 1e9}
+        if best is None or row["gbps"] > best["gbps"]:
+            best = row
+    return best
+
+
 # ---- CLI (bench_decode.cu:213-326) ------------------------------------------
 
 HEADER = "gpu,dtype,batch,seq_len,hq,hkv,dim,page,ctas,segments,time_us,gbps,pct_peak"
