@@ -259,7 +259,8 @@ int run(const Args& a) {
         HIP_CHECK(hipGetDevice(&dev));
         HIP_CHECK(hipGetDeviceProperties(&prop, dev));
         g.name = prop.name;
-        if (g.name.empty()) {   // the marketing name needs libdrm's id table; fall back to the ISA name
+        if (g.name.empty() || g.name == "AMD Radeon Graphics") {   // the marketing name needs libdrm's id
+                                                                    // table; fall back to the ISA name
             const std::string arch = prop.gcnArchName;
             g.name = "AMD " + arch.substr(0, arch.find(':'));
         }

@@ -367,7 +367,10 @@ def main(argv: list[str] | None = None) -> int:
     geti = lambda k, d: int(a.get(k, d))   # noqa: E731
     core.load()
     props = torch.cuda.get_device_properties(0)
-    gpu = props.name.replace(",", " ")
+    gpu = props.name
+    if not gpu or gpu == "AMD Radeon Graphics":   # the runtime's name when libdrm's id table is absent
+        gpu = "AMD " + props.gcnArchName.split(":")[0]
+    gpu = gpu.replace(",", " ")
     cus = props.multi_processor_count
     peak = float(a.get("peak-gbps", PEAK_GBPS))
     print(f"# {gpu}, {cus} CUs, HBM peak {peak:.0f} GB/s", file=sys.stderr, flush=True)
