@@ -208,6 +208,17 @@ def copy_rows(cus: int, iters: int = 10, nbytes: int = 4 << 30) -> list[dict]:
     return rows
 
 
+def gpu_name() -> str:
+    """The device name for CSV rows: the runtime's, or the ISA name when the
+    runtime only has a generic one (its marketing names need libdrm's id table)."""
+    import torch
+    props = torch.cuda.get_device_properties(0)
+    name = props.name
+    if not name or name == "AMD Radeon Graphics":
+        name = "AMD " + props.gcnArchName.split(":")[0]
+    return name.replace(",", " ")
+
+
 def chunked_read_same_bytes(cus: int, nbytes: int, iters: int = 10) -> dict | None:
     """The best chunked streaming read (one contiguous span per wave) of about
     `nbytes` (rounded down to what the span shapes divide): the read ceiling at
@@ -367,10 +378,7 @@ def main(argv: list[str] | None = None) -> int:
     geti = lambda k, d: int(a.get(k, d))   # noqa: E731
     core.load()
     props = torch.cuda.get_device_properties(0)
-    gpu = props.name
-    if not gpu or gpu == "AMD Radeon Graphics":   # the runtime's name when libdrm's id table is absent
-        gpu = "AMD " + props.gcnArchName.split(":")[0]
-    gpu = gpu.replace(",", " ")
+    gpu = gpu_name()
     cus = props.multi_processor_count
     peak = float(a.get("peak-gbps", PEAK_GBPS))
     print(f"# {gpu}, {cus} CUs, HBM peak {peak:.0f} GB/s", file=sys.stderr, flush=True)

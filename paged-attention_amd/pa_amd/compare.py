@@ -125,7 +125,7 @@ def rows(shapes=SHAPES, iters: int = 50, repeats: int = 1, dtypes=(False, True),
     """Yields one dict per (dtype, shape), in compare_flashinfer.py's order (all
     fp16 shapes, then all FP8 shapes, so every FP8 row has its fp16 twin)."""
     from torch.nn.attention import SDPBackend
-    gpu = torch.cuda.get_device_name(0).replace(",", " ")
+    gpu = bench_decode.gpu_name()
     flusher = bench_decode.Flusher()
     fp16_out = {}
     for fp8 in dtypes:
@@ -186,7 +186,7 @@ def main(argv=None) -> int:
     ap.add_argument("--peak-gbps", type=float, default=bench_decode.PEAK_GBPS)
     args = ap.parse_args(argv)
     core.load()
-    print(f"# {torch.cuda.get_device_name(0)}, torch {torch.__version__}, peak {args.peak_gbps} GB/s",
+    print(f"# {bench_decode.gpu_name()}, torch {torch.__version__}, peak {args.peak_gbps} GB/s",
           file=sys.stderr, flush=True)
     print(HEADER, flush=True)
     shapes = QUICK if args.quick else SHAPES
