@@ -112,10 +112,11 @@ def test_many_short_rows(fp8):
 def test_pages_beyond_4gib_of_pool(fp8):
     """Pools larger than 4 GiB: the same sequence stored in the first pages
     and in pages past the 4 GiB mark of each pool decodes to the same bits
-    (64-bit page offsets in every load path: power-of-two and per-lane)."""
+    (64-bit page offsets in every load path: power-of-two, staged small
+    pages and per-lane)."""
     import torch
     hq, hkv = 32, 8
-    for P in (16, 5):
+    for P in (16, 8, 5):
         page_bytes = hkv * P * D * (1 if fp8 else 2)
         pages = (4 << 30) // page_bytes + 4096                 # the last pages start past 4 GiB
         dt = torch.uint8 if fp8 else torch.float16
