@@ -112,8 +112,10 @@ pa_status pa_plan_build_tiled(int tile, const int32_t* seq_lens, int batch, int 
 /* A plan from caller-built host arrays (decode.hpp:21-27 DecodePlan's fields),
  * validated: prefix arrays rise from 0 to num_segments, every segment is
  * non-empty and listed under its (row, kv head) item = row * num_kv_heads +
- * head, and every item has a segment. num_kv_heads = 0 infers it (1 + the
- * largest head in the segments). Lets DevicePlan::upload take any DecodePlan. */
+ * head, every item has a segment and every segment starts on a multiple of 16
+ * tokens (the kernels' step; the reference's plans start on its 64-token
+ * tiles). num_kv_heads = 0 infers it (1 + the largest head in the segments).
+ * Lets DevicePlan::upload take any DecodePlan. */
 pa_status pa_plan_create(int num_ctas, int tile, const int32_t* segments, int num_segments,
                          const int32_t* cta_seg_begin, const int32_t* item_seg_begin, int num_items,
                          int num_kv_heads, pa_plan** out);
@@ -132,7 +134,8 @@ typedef struct pa_device_plan pa_device_plan;   /* decode.hpp:44-63 DevicePlan *
 pa_status pa_device_plan_create(pa_device_plan** out);
 void      pa_device_plan_destroy(pa_device_plan* dp);
 /* decode.cu:131-146 DevicePlan::upload: grow-only device copies of the plan plus
- * the partial workspace (segments * group * (head_dim + 1) floats). */
+ * the partial workspace (segments * group * (head_dim + 1) floats). Rejects a
+ * plan whose segments do not start on multiples of 16 tokens. */
 pa_status pa_device_plan_upload(pa_device_plan* dp, const pa_plan* plan, int group, int head_dim,
                                 void* stream);
 /* decode.cu:148-156 DevicePlan::bind: points the schedule fields of *p at it. */

@@ -116,6 +116,11 @@ void make_plan_impl(pa_plan& plan, int dtype, const int32_t* lens, int batch, in
 void device_plan_upload(pa_device_plan& dp, const pa_plan& plan, int group, int head_dim, hipStream_t s) {
     if (group <= 0 || head_dim <= 0) throw std::invalid_argument("upload: bad group or head_dim");
     const size_t nseg = plan.segments.size() / 4;
+    // The kernels read a 16-token group from one page run (page sizes >= 16) or
+    // one 1 KiB part from one page: a segment may only start on a group boundary.
+    for (size_t i = 0; i < nseg; ++i)
+        if (plan.segments[4 * i + 2] % pa::kGroupTokens != 0)
+            throw std::invalid_argument("upload: segment starts must be multiples of 16 tokens");
     upload_grow(dp.segments, dp.seg_cap, plan.segments.data(), plan.segments.size(), s);
     upload_grow(dp.cta_seg_begin, dp.cta_cap, plan.cta_seg_begin.data(), plan.cta_seg_begin.size(), s);
     upload_grow(dp.item_seg_begin, dp.item_cap, plan.item_seg_begin.data(), plan.item_seg_begin.size(), s);
@@ -274,6 +279,8 @@ pa_status pa_plan_create(int num_ctas, int tile, const int32_t* segments, int nu
             if (sg[0] < 0 || sg[1] < 0 || sg[1] >= num_kv_heads || item >= num_items)
                 throw std::invalid_argument("plan: segment row / kv head out of range");
             if (sg[2] < 0 || sg[3] <= sg[2]) throw std::invalid_argument("plan: empty or negative segment");
+            if (sg[2] % pa::kGroupTokens != 0)
+                throw std::invalid_argument("plan: segment starts must be multiples of 16 tokens");
             if (i < item_seg_begin[item] || i >= item_seg_begin[item + 1])
                 throw std::invalid_argument("plan: segment is not listed under its (row, kv head)");
         }

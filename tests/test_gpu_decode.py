@@ -192,6 +192,18 @@ def test_block_merge_and_merge_kernel_agree(fp8):
         assert float(np.max(np.abs(o - ref))) < TOL
     assert float(np.max(np.abs(outs[0] - outs[1]))) < 1e-3
 
+def test_device_plan_rejects_unaligned_segment_starts():
+    """A plan cut at 8-token tiles has segments starting off the kernels'
+    16-token groups; DevicePlan::upload refuses it instead of letting a group
+    read across a page boundary."""
+    plan = pa_amd.make_plan_tiled(8, [100, 37], 8, 64)
+    assert any(int(s[2]) % 16 for s in plan.segments)
+    dplan = pa_amd.DevicePlan()
+    with pytest.raises(pa_amd.InvalidArgument):
+        dplan.upload(plan, 4, D)
+    ok = pa_amd.make_plan_tiled(16, [100, 37], 8, 64)
+    dplan.upload(ok, 4, D)
+
 @pytest.mark.parametrize("group", [1, 2, 4, 8])
 @pytest.mark.parametrize("fp8", DTYPES, ids=IDS)
 def test_block_merge_two_split_segments_per_unit(fp8, group):

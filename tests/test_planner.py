@@ -136,6 +136,11 @@ def test_plan_create_accepts_built_plans_and_rejects_broken_ones():
     bad = dict(good, cta=built.cta_seg_begin.copy())
     bad["cta"][1], bad["cta"][2] = bad["cta"][2], bad["cta"][1]   # falling prefix
     assert _create(bad) == 1 or np.all(np.diff(bad["cta"]) >= 0)
+    bad = dict(good, segments=built.segments.copy())
+    i = int(np.argmax(built.segments[:, 3] - built.segments[:, 2]))
+    assert built.segments[i, 3] - built.segments[i, 2] > 16
+    bad["segments"][i, 2] += 8                                     # starts off a 16-token boundary
+    assert _create(bad) == 1
     bad = dict(good, item=built.item_seg_begin.copy())
     bad["item"][-1] += 1                                           # does not end at num_segments
     assert _create(bad) == 1
