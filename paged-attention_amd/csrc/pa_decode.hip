@@ -60,7 +60,7 @@
 #include <type_traits>
 
 // Compile-time tuning knobs, per cache element type.
-// Tokens per step of the power-of-two page path (16 or 32).
+// Tokens per step (16 or 32), the same on every page path.
 #ifndef PA_FP16_STEP
 #define PA_FP16_STEP 16
 #endif
@@ -134,7 +134,8 @@ static_assert(Tune<1>::step == 16 || Tune<1>::step == 32, "fp8 step must be 16 o
 // How a step finds its pages.
 enum PagePath : int {
     kPagePow2 = 0,   // page_size a power of two >= 16: a 16-token half is in one page
-    kPageQuad = 1,   // page_size 4 or 8: one lookup per lane for K and one for V
+    kPageQuad = 1,   // FP8 page_size 4 (8 without the LDS stage): one lookup per lane for
+                     // K and one for V
     kPageAny  = 2,   // any other page size: one lookup per token, integer division
     kPageRuns = 3,   // page_size 4 or 8 (fp16) / 8 (FP8 with the LDS stage): K/V through
                      // the LDS stage, one wave-uniform page per coalesced 1 KiB part
