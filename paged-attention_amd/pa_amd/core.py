@@ -39,6 +39,9 @@ def _stream(stream) -> int | None:
     if stream is None:
         import torch
         if torch.cuda.is_available():
+            raw = getattr(torch._C, "_cuda_getCurrentRawStream", None)   # no Stream object: ~0.1 us
+            if raw is not None:
+                return raw(torch.cuda.current_device())
             return torch.cuda.current_stream().cuda_stream
         return None
     if isinstance(stream, int):
