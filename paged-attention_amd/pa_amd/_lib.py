@@ -205,6 +205,3 @@ def call(name: str, *args):
     """Calls a status-returning entry point and raises on failure."""
     check(getattr(load(), name)(*args))
 
-
-def dtype_code(fp8: bool) -> int:
-    return PA_KV_FP8_E4M3 if fp8 else PA_KV_FP16

@@ -33,8 +33,6 @@ import math
 import statistics
 import sys
 
-import numpy as np
-
 from . import core
 from ._lib import InvalidArgument
 

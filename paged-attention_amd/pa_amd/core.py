@@ -16,7 +16,7 @@ from dataclasses import dataclass
 import numpy as np
 
 from . import _lib
-from ._lib import CacheConfig, DecodeParams, InvalidArgument, call, check, dtype_code, load
+from ._lib import CacheConfig, DecodeParams, InvalidArgument, call, check, load
 
 FP16 = _lib.PA_KV_FP16
 FP8_E4M3 = _lib.PA_KV_FP8_E4M3

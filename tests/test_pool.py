@@ -9,7 +9,6 @@ the allocator until it is full, as bench_decode.cu:291-325 does.
 import csv
 import pathlib
 
-import numpy as np
 import pytest
 
 import pa_amd
