@@ -53,6 +53,7 @@
 
 #include "pa_device.hpp"
 
+#include <algorithm>
 #include <cmath>
 #include <cstdint>
 #include <stdexcept>
@@ -188,6 +189,19 @@ __device__ __forceinline__ float head_pick(const float (&arr)[G], int kb, int i)
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, int bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, kBufferFlags);
+}
+
+// One normalized O row (head row i of the lane's accumulators) of a split
+// segment into a partial row: lane c holds dims 8c .. 8c+7.
+__device__ __forceinline__ void store_row(float* row, const f32x4 (&oacc)[8], int i, float inv, int c) {
+    f32x4 lo, hi;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        lo[j] = oacc[j][i] * inv;
+        hi[j] = oacc[4 + j][i] * inv;
+    }
+    *reinterpret_cast<f32x4*>(row + 8 * c)     = lo;
+    *reinterpret_cast<f32x4*>(row + 8 * c + 4) = hi;
 }
 
 // Block-level merge after the split loop. slot_item holds, per wave, the
@@ -502,6 +516,7 @@ __device__ __forceinline__ void decode_split_body(const pa_decode_params& p, int
 #pragma unroll
                 for (int i = 0; i < HW; ++i) {
                     const float inv = p.v_scale / head_pick<G>(inv_h, kb, i);
+                    uint16_t* orow = p.out + (static_cast<size_t>(C.b) * hq + C.h * G + 4 * kb + i) * kHeadDim;
                     u32x4 o;
 #pragma unroll
                     for (int jj = 0; jj < 4; ++jj) {
@@ -509,8 +524,7 @@ __device__ __forceinline__ void decode_split_body(const pa_decode_params& p, int
                                           static_cast<_Float16>(oacc[2 * jj + 1][i] * inv)};
                         o[jj] = __builtin_bit_cast(uint32_t, h2);
                     }
-                    *reinterpret_cast<u32x4*>(p.out + (static_cast<size_t>(C.b) * hq + C.h * G + 4 * kb + i) *
-                                                          kHeadDim + 8 * c) = o;
+                    *reinterpret_cast<u32x4*>(orow + 8 * c) = o;
                 }
             } else {
                 const int sl = C.seg == seg_begin ? 0 : 1;   // a unit's split segments are its first and last
@@ -519,21 +533,15 @@ __device__ __forceinline__ void decode_split_body(const pa_decode_params& p, int
                     const float lh  = head_pick<G>(inv_h, kb, i);
                     const float inv = p.v_scale / lh;
                     const float ls  = head_pick<G>(m_h, kb, i) + __log2f(lh);
-                    f32x4 lo, hi;
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        lo[j] = oacc[j][i] * inv;
-                        hi[j] = oacc[4 + j][i] * inv;
-                    }
+                    // The LDS and HBM stores stay in separate branches: a pointer
+                    // selected between them would be a generic (flat) address.
                     if (merge_here) {
-                        float* lrow = &part_lds[2 * wave + sl][(4 * kb + i) * kHeadDim + 8 * c];
-                        *reinterpret_cast<f32x4*>(lrow)     = lo;
-                        *reinterpret_cast<f32x4*>(lrow + 4) = hi;
+                        float* lrow = &part_lds[2 * wave + sl][(4 * kb + i) * kHeadDim];
+                        store_row(lrow, oacc, i, inv, c);
                         if (c == 0) lse_lds[2 * wave + sl][4 * kb + i] = ls;
                     } else {
-                        float* prow = p.partial_out + (static_cast<size_t>(C.seg) * G + 4 * kb + i) * kHeadDim + 8 * c;
-                        *reinterpret_cast<f32x4*>(prow)     = lo;
-                        *reinterpret_cast<f32x4*>(prow + 4) = hi;
+                        float* prow = p.partial_out + (static_cast<size_t>(C.seg) * G + 4 * kb + i) * kHeadDim;
+                        store_row(prow, oacc, i, inv, c);
                         if (c == 0) p.partial_lse[static_cast<size_t>(C.seg) * G + 4 * kb + i] = ls;
                     }
                 }
@@ -998,7 +1006,12 @@ int kernel_units_per_cu(int dtype, int group) {
     int blocks = 0;
     hip_check(hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, fn, 64 * kWaves, 0),
               "hipOccupancyMaxActiveBlocksPerMultiprocessor");
-    return blocks * kWaves;
+    // At most the waves per SIMD the kernel is tuned for (4 SIMDs per CU): a
+    // build that happens to fit more (fewer registers) keeps the measured
+    // best grid, since more concurrent streams per CU read HBM less
+    // efficiently.
+    const int tuned = 4 * (fp16 ? PA_FP16_WAVES_PER_EU : PA_FP8_WAVES_PER_EU) / kWaves;
+    return std::max(1, std::min(blocks, tuned)) * kWaves;
 }
 
 hipError_t launch_decode_split(int dtype, const pa_decode_params& p, hipStream_t s) {

@@ -192,6 +192,17 @@ def test_block_merge_and_merge_kernel_agree(fp8):
         assert float(np.max(np.abs(o - ref))) < TOL
     assert float(np.max(np.abs(outs[0] - outs[1]))) < 1e-3
 
+def test_persistent_grid_is_two_waves_per_simd():
+    """The default grid is 8 work units (2 waves per SIMD) per CU for every
+    dtype and group, whatever the kernels' register counts would let the
+    hardware hold: more concurrent streams per CU read HBM less efficiently."""
+    import torch
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    for dt in (pa_amd.FP16, pa_amd.FP8_E4M3):
+        for g in (1, 2, 4, 8):
+            assert pa_amd.wave_ctas(dt, D, g) == 8 * cus
+    assert pa_amd.make_plan(pa_amd.FP16, [8192] * 32, 32, 8, D, 0).num_ctas == 8 * cus
+
 def test_device_plan_rejects_unaligned_segment_starts():
     """A plan cut at 8-token tiles has segments starting off the kernels'
     16-token groups; DevicePlan::upload refuses it instead of letting a group
