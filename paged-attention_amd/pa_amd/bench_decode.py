@@ -370,9 +370,17 @@ def run_one(gpu: str, peak: float, fl: Flusher | None, s: Setup, ctas: int, iter
     return row
 
 
+MODES = ("sweep", "ctas", "pagesize", "capacity", "copy", "single", "append")
+
+
 def main(argv: list[str] | None = None) -> int:
+    args = sys.argv[1:] if argv is None else argv
+    mode, a = _parse(args)
+    if "help" in a or "h" in a or "-h" in args or mode not in MODES:
+        # Usage needs no device (the reference prints it before touching CUDA).
+        print(__doc__, file=sys.stdout if mode in MODES else sys.stderr)
+        return 0 if mode in MODES else 2
     import torch
-    mode, a = _parse(sys.argv[1:] if argv is None else argv)
     geti = lambda k, d: int(a.get(k, d))   # noqa: E731
     core.load()
     props = torch.cuda.get_device_properties(0)

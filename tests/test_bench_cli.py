@@ -57,3 +57,18 @@ def test_capacity_rows_match_reference():
     key = lambda r: (r["dtype"], r["layout"], r["actual_len"])   # noqa: E731
     assert {key(r): (r["sequences"], r["bytes_per_seq"]) for r in got} == \
         {key(r): (r["sequences"], r["bytes_per_seq"]) for r in want}
+
+
+def test_python_twin_help_needs_no_device():
+    """`python -m pa_amd.bench_decode --help` prints the usage without touching a
+    GPU (as the native CLI does); an unknown mode exits 2."""
+    import sys
+    cwd = ROOT / "paged-attention_amd"
+    r = subprocess.run([sys.executable, "-m", "pa_amd.bench_decode", "--help"], capture_output=True, text=True,
+                       timeout=120, cwd=cwd)
+    assert r.returncode == 0
+    for mode in ("sweep", "ctas", "pagesize", "capacity", "copy", "single", "append"):
+        assert mode in r.stdout
+    r = subprocess.run([sys.executable, "-m", "pa_amd.bench_decode", "nosuchmode"], capture_output=True, text=True,
+                       timeout=120, cwd=cwd)
+    assert r.returncode == 2
