@@ -135,11 +135,15 @@ static_assert(Tune<1>::step == 16 || Tune<1>::step == 32, "fp8 step must be 16 o
 // How a step finds its pages.
 enum PagePath : int {
     kPagePow2 = 0,   // page_size a power of two >= 16: a 16-token half is in one page
-    kPageQuad = 1,   // FP8 page_size 4 (8 without the LDS stage): one lookup per lane for
-                     // K and one for V
-    kPageAny  = 2,   // any other page size: one lookup per token, integer division
+    kPageQuad = 1,   // FP8 without the LDS stage, page_size 4 or 8: one lookup per lane
+                     // for K and one for V
+    kPageAny  = 2,   // FP8 without the LDS stage, any other page size: one lookup per
+                     // token, integer division
     kPageRuns = 3,   // page_size 4 or 8 (fp16) / 8 (FP8 with the LDS stage): K/V through
                      // the LDS stage, one wave-uniform page per coalesced 1 KiB part
+    kPageLane = 4,   // every other page size (1, 2, FP8 4, any non-power of two): K/V
+                     // through the LDS stage, each lane finding the page of the row it
+                     // loads (coalesced 16-byte loads at per-lane addresses)
 };
 
 // One position of a wave's schedule: the current step of the current segment.
@@ -279,7 +283,8 @@ __device__ __forceinline__ void decode_split_body(const pa_decode_params& p, int
     constexpr int  NQ    = G > 4 ? 2 : 1;           // compact Q registers per lane
     constexpr int  NVL   = PATH == kPageAny ? 4 : 1;   // V page lookups per lane (per-lane paths)
     constexpr int  HW    = G < 4 ? G : 4;           // live O rows per writing lane
-    constexpr bool STG   = PATH == kPageRuns || (Tune<EB>::stage && PATH == kPagePow2);   // K/V via LDS
+    constexpr bool STG   = PATH == kPageRuns || PATH == kPageLane ||
+                           (Tune<EB>::stage && PATH == kPagePow2);   // K/V via LDS
     constexpr int  RPP   = 1024 / ROW;              // rows per coalesced 1 KiB part (4 fp16, 8 FP8)
     constexpr int  NPART = 16 / RPP;                // parts per 16-token half
     constexpr int  CPR   = ROW / 16;                // 16-byte chunks per row
@@ -334,6 +339,8 @@ __device__ __forceinline__ void decode_split_body(const pa_decode_params& p, int
     u32x4 qc[DEPTH][NQ];       // compact Q, loaded with a segment's first step
     int   pg[DEPTH][NH];       // power-of-two path: page of each half (wave-uniform)
     int   pgr[PATH == kPageRuns ? DEPTH : 1][NH][NPART];   // small pages: page of each part
+    constexpr int LN = PATH == kPageLane ? DEPTH : 1;
+    int   plk[LN][NH][NPART], psl[LN][NH][NPART];          // lane path: page and slot of the lane's row
     int   pk[DEPTH][NH], sk[DEPTH][NH];            // per-lane paths: K token's page and slot
     int   pv[DEPTH][NH][NVL], sv[DEPTH][NH][NVL];  // per-lane paths: V tokens' page(s) and slot(s)
 
@@ -360,6 +367,20 @@ __device__ __forceinline__ void decode_split_body(const pa_decode_params& p, int
                     for (int part = 0; part < NPART; ++part)
                         pgr[s][hh][part] = t_row[min(T.tok + 16 * hh + RPP * part, T.w - 1) >> page_shift];
             }
+        } else if constexpr (PATH == kPageLane) {
+            // The row this lane loads in each 1 KiB part; like the other
+            // per-lane paths, lookups repeat T's last step once it is
+            // exhausted, so that every slot issues the same vector loads.
+            const int last = T.w - 1;
+#pragma unroll
+            for (int hh = 0; hh < NH; ++hh)
+#pragma unroll
+                for (int part = 0; part < NPART; ++part) {
+                    const int tk = min(T.tok + 16 * hh + RPP * part + lane / CPR, last);
+                    const int qk = page_shift >= 0 ? tk >> page_shift : tk / P;   // wave-uniform choice
+                    plk[s][hh][part] = t_row[qk];
+                    psl[s][hh][part] = tk - qk * P;
+                }
         } else {
             // Per-lane lookups repeat T's last step once it is exhausted, so
             // that every slot issues the same vector loads.
@@ -464,6 +485,16 @@ __device__ __forceinline__ void decode_split_body(const pa_decode_params& p, int
                         u32x4, __builtin_amdgcn_raw_buffer_load_b128(krs, 16 * lane, 0, kAux<NT>));
                     vc[s][hh][part] = __builtin_bit_cast(
                         u32x4, __builtin_amdgcn_raw_buffer_load_b128(vrs, 16 * lane, 0, kAux<NT>));
+                }
+        } else if constexpr (PATH == kPageLane) {
+#pragma unroll
+            for (int hh = 0; hh < NH; ++hh)
+#pragma unroll
+                for (int part = 0; part < NPART; ++part) {
+                    const size_t off =
+                        kv_row_offset<EB>(plk[s][hh][part], L.h, psl[s][hh][part], P, hkv) + 16 * (lane % CPR);
+                    kc[s][hh][part] = load16<NT>(kbase + off);
+                    vc[s][hh][part] = load16<NT>(vbase + off);
                 }
         } else {
 #pragma unroll
@@ -882,7 +913,8 @@ __global__ __launch_bounds__(64 * WAVES) void decode_merge_kernel(const pa_decod
 // Dispatch.
 
 // Steps in flight on the per-lane page paths (they keep the power-of-two
-// path's step, so results do not depend on the page size).
+// path's step, so results do not depend on the page size): kPageLane, and
+// kPageQuad / kPageAny in FP8 builds without the LDS stage.
 #ifndef PA_FP16_LANE_DEPTH
 #define PA_FP16_LANE_DEPTH 1
 #endif
@@ -914,16 +946,19 @@ hipError_t launch_split_g(const pa_decode_params& p, hipStream_t s) {
             throw std::invalid_argument("decode: page_size * num_kv_heads * row bytes must be below 2^31");
         return launch_split_p<EB, G, Tune<EB>::step, Tune<EB>::depth, kPagePow2>(p, shift, s);
     }
-    // Pages of whole 1 KiB parts (4 fp16 rows, 8 FP8 rows) through the LDS stage.
-    if (P == 8 || (EB == 2 && P == 4)) {
-        if constexpr (EB == 2 || Tune<EB>::stage) {
+    if constexpr (EB == 2 || Tune<EB>::stage) {
+        // Pages of whole 1 KiB parts (4 fp16 rows, 8 FP8 rows) through the LDS stage.
+        if (P == 8 || (EB == 2 && P == 4)) {
             if (static_cast<long long>(p.num_kv_heads) * P * kRowBytes<EB> >= (1ll << 31))
                 throw std::invalid_argument("decode: page_size * num_kv_heads * row bytes must be below 2^31");
             return launch_split_p<EB, G, Tune<EB>::step, Tune<EB>::depth, kPageRuns>(p, shift, s);
         }
+        // Any other size: per-lane rows through the LDS stage (shift -1: divide).
+        return launch_split_p<EB, G, Tune<EB>::step, kLaneDepth<EB>, kPageLane>(p, pow2 ? shift : -1, s);
+    } else {
+        if (pow2 && P >= 4) return launch_split_p<EB, G, Tune<EB>::step, kLaneDepth<EB>, kPageQuad>(p, shift, s);
+        return launch_split_p<EB, G, Tune<EB>::step, kLaneDepth<EB>, kPageAny>(p, shift, s);
     }
-    if (pow2 && P >= 4) return launch_split_p<EB, G, Tune<EB>::step, kLaneDepth<EB>, kPageQuad>(p, shift, s);
-    return launch_split_p<EB, G, Tune<EB>::step, kLaneDepth<EB>, kPageAny>(p, shift, s);
 }
 
 template <int EB>

@@ -41,7 +41,7 @@ def test_mixed_length_batch(fp8):
     assert err < TOL, err
 
 @pytest.mark.parametrize("fp8", DTYPES, ids=IDS)
-@pytest.mark.parametrize("page_size", [1, 3, 4, 8, 16, 32, 128])
+@pytest.mark.parametrize("page_size", [1, 2, 3, 4, 6, 8, 16, 32, 128])
 def test_page_sizes(fp8, page_size):
     err, _, _ = run_cache_case(fp8, 16, 4, page_size, [300, 2500])
     assert err < TOL, err
