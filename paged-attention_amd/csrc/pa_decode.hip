@@ -340,7 +340,9 @@ __device__ __forceinline__ void decode_split_body(const pa_decode_params& p, int
     int   pg[DEPTH][NH];       // power-of-two path: page of each half (wave-uniform)
     int   pgr[PATH == kPageRuns ? DEPTH : 1][NH][NPART];   // small pages: page of each part
     constexpr int LN = PATH == kPageLane ? DEPTH : 1;
-    int   plk[LN][NH][NPART], psl[LN][NH][NPART];          // lane path: page and slot of the lane's row
+    int   plk[LN][NH][NPART], psl[LN][NH][NPART];          // lane path: byte address of the lane holding
+                                                           // the row's page entry, slot in the page
+    int   pent[LN];                                        // lane path: table entry `first page + lane`
     int   pk[DEPTH][NH], sk[DEPTH][NH];            // per-lane paths: K token's page and slot
     int   pv[DEPTH][NH][NVL], sv[DEPTH][NH][NVL];  // per-lane paths: V tokens' page(s) and slot(s)
 
@@ -368,17 +370,23 @@ __device__ __forceinline__ void decode_split_body(const pa_decode_params& p, int
                         pgr[s][hh][part] = t_row[min(T.tok + 16 * hh + RPP * part, T.w - 1) >> page_shift];
             }
         } else if constexpr (PATH == kPageLane) {
-            // The row this lane loads in each 1 KiB part; like the other
-            // per-lane paths, lookups repeat T's last step once it is
-            // exhausted, so that every slot issues the same vector loads.
-            const int last = T.w - 1;
+            // One table read per lane covers the step's pages (at most
+            // NG / P + 1 <= 33 entries); each lane then needs the page of the
+            // row it loads in each 1 KiB part, fetched from the lane holding
+            // it with ds_bpermute at issue time. Like the other per-lane
+            // paths, lookups repeat T's last step once it is exhausted, so
+            // that every slot issues the same vector loads.
+            const int last  = T.w - 1;
+            const int first = page_shift >= 0 ? T.tok >> page_shift : T.tok / P;   // wave-uniform choice
+            const int lastp = page_shift >= 0 ? last >> page_shift : last / P;
+            pent[s] = t_row[min(first + lane, lastp)];
 #pragma unroll
             for (int hh = 0; hh < NH; ++hh)
 #pragma unroll
                 for (int part = 0; part < NPART; ++part) {
                     const int tk = min(T.tok + 16 * hh + RPP * part + lane / CPR, last);
-                    const int qk = page_shift >= 0 ? tk >> page_shift : tk / P;   // wave-uniform choice
-                    plk[s][hh][part] = t_row[qk];
+                    const int qk = page_shift >= 0 ? tk >> page_shift : tk / P;
+                    plk[s][hh][part] = 4 * (qk - first);
                     psl[s][hh][part] = tk - qk * P;
                 }
         } else {
@@ -491,8 +499,8 @@ __device__ __forceinline__ void decode_split_body(const pa_decode_params& p, int
             for (int hh = 0; hh < NH; ++hh)
 #pragma unroll
                 for (int part = 0; part < NPART; ++part) {
-                    const size_t off =
-                        kv_row_offset<EB>(plk[s][hh][part], L.h, psl[s][hh][part], P, hkv) + 16 * (lane % CPR);
+                    const int pgl = __builtin_amdgcn_ds_bpermute(plk[s][hh][part], pent[s]);
+                    const size_t off = kv_row_offset<EB>(pgl, L.h, psl[s][hh][part], P, hkv) + 16 * (lane % CPR);
                     kc[s][hh][part] = load16<NT>(kbase + off);
                     vc[s][hh][part] = load16<NT>(vbase + off);
                 }
