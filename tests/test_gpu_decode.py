@@ -36,6 +36,16 @@ def test_gqa_groups(fp8, hq, hkv):
     assert err < TOL, err
 
 @pytest.mark.parametrize("fp8", DTYPES, ids=IDS)
+@pytest.mark.parametrize("hq,hkv", [(8, 8), (8, 4), (8, 1)])
+@pytest.mark.parametrize("page_size", [1, 3, 4])
+def test_small_pages_every_group(fp8, hq, hkv, page_size):
+    """The per-lane staged page path (page sizes 1, 2, FP8 4 and non-powers
+    of two) for GQA groups 1, 2 and 8, with a ragged batch whose rows end
+    inside a step."""
+    err, _, _ = run_cache_case(fp8, hq, hkv, page_size, [5, 333, 1027])
+    assert err < TOL, err
+
+@pytest.mark.parametrize("fp8", DTYPES, ids=IDS)
 def test_mixed_length_batch(fp8):
     err, _, _ = run_cache_case(fp8, 32, 8, 16, [1, 15, 16, 17, 129, 1000, 4099])
     assert err < TOL, err
