@@ -21,6 +21,11 @@ Pinning (what checks each function; the tests are named in parentheses):
   paged_decode     float64 numpy attention on tiny inputs, GQA mapping and
                    permutation invariance (test_oracle_attention)
   append/gather    closed-form address on brute-force tiny pools (test_oracle_paging)
+  e4m3 table       equal to orc_append's FP8 store for all 65536 fp16 codes at
+                   several scales (test_oracle_paging)
+  attention_pairs  every (row, query head) pair equal to paged_decode and to
+                   cpu_attention on the same gathered inputs, with and without
+                   the reference's compiled cpu_attention (test_oracle_attention)
   make_plan        68 (ctas, segments) rows of the reference's results/*.csv,
                    fixture tests/golden/planner_rows.csv (test_planner)
 """
@@ -71,6 +76,7 @@ def lib() -> ctypes.CDLL:
         L.orc_f32_to_f16_array.argtypes = [_P, _P, ctypes.c_size_t]
         L.orc_f16_to_f32_array.argtypes = [_P, _P, ctypes.c_size_t]
         L.orc_append.argtypes = [_I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _F]
+        L.orc_e4m3_quantize_table.argtypes = [_F, _P]
         L.orc_gather_raw.argtypes = [_I, _P, _P, _I, _I, _I, _I, _I, _P]
         L.orc_gather_dequant.argtypes = [_I, _P, _P, _I, _I, _I, _I, _I, _F, _P]
         L.orc_cpu_attention.argtypes = [_P, _P, _P, _P, _I, _I]
@@ -135,6 +141,14 @@ def append(dtype: int, k: np.ndarray, v: np.ndarray, k_cache: np.ndarray, v_cach
     assert k_cache.flags.c_contiguous and v_cache.flags.c_contiguous
     lib().orc_append(dtype, k.ctypes.data, v.ctypes.data, k_cache.ctypes.data, v_cache.ctypes.data,
                      bt.ctypes.data, start_pos, n, hkv, hd, page_size, inv_k, inv_v)
+
+
+def e4m3_quantize_table(inv_scale: float) -> np.ndarray:
+    """uint8[65536]: the E4M3 byte orc_append stores for each fp16 code at
+    reciprocal scale inv_scale (index the table with the fp16 bit patterns)."""
+    out = np.zeros(65536, dtype=np.uint8)
+    lib().orc_e4m3_quantize_table(float(inv_scale), out.ctypes.data)
+    return out
 
 
 def gather_raw(dtype: int, cache: np.ndarray, bt_row: np.ndarray, hkv: int, hd: int,

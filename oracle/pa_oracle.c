@@ -129,6 +129,10 @@ void orc_append(int dtype, const uint16_t* k, const uint16_t* v, void* k_cache, 
     }
 }
 
+void orc_e4m3_quantize_table(float inv_scale, uint8_t* out) {
+    for (uint32_t h = 0; h < 65536u; h++) out[h] = orc_f32_to_e4m3(orc_f16_to_f32((uint16_t)h) * inv_scale);
+}
+
 void orc_gather_raw(int dtype, const void* cache, const int32_t* bt_row, int hkv, int hd,
                     int page_size, int h, int len, void* out) {
     const size_t eb = dtype == 0 ? 2 : 1;

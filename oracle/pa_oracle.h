@@ -39,6 +39,11 @@ void orc_append(int dtype, const uint16_t* k, const uint16_t* v, void* k_cache, 
                 const int32_t* bt_row, int start_pos, int n, int hkv, int hd, int page_size,
                 float inv_k_scale, float inv_v_scale);
 
+/* The FP8 store of orc_append as a table: out[h] = e4m3(float(fp16 code h) *
+ * inv_scale) for all 65536 fp16 codes h (paged_kv_cache.cu:20-22 at one fixed
+ * scale). Lets a check of a large FP8 pool look each stored byte up. */
+void orc_e4m3_quantize_table(float inv_scale, uint8_t* out);
+
 /* decode_kernels.cuh:175-177 address resolution; raw element bytes of tokens
  * [0,len) of kv head h into out ([len][hd] elements). */
 void orc_gather_raw(int dtype, const void* cache, const int32_t* bt_row, int hkv, int hd,

@@ -615,9 +615,11 @@ __device__ __forceinline__ void decode_split_body(const pa_decode_params& p, int
         if (__builtin_expect(C.tok == C.t0, 0)) {
             // Q of the new segment: compact -> LDS -> B-operand layout.
             u32x4* ql = q_lds[wave];
+            wave_lds_sync();   // the previous segment's Q reads are done
 #pragma unroll
             for (int n = 0; n < NQ; ++n)
                 if (64 * n + lane < 16 * G) ql[64 * n + lane] = qc[s][n];
+            wave_lds_sync();   // every lane's Q write lands before any lane reads
             const int hc = c & (G - 1);
 #pragma unroll
             for (int j = 0; j < 4; ++j) qf[j] = ql[16 * hc + (KNAT ? 4 * j + kb : 4 * kb + j)];
@@ -629,6 +631,7 @@ __device__ __forceinline__ void decode_split_body(const pa_decode_params& p, int
             // -> the K / V lane layouts of the direct loads.
             u32x4* st = stage_lds[wave];
             const int wrow = lane / CPR;   // row within a 1 KiB part
+            wave_lds_sync();   // the previous step's stage reads are done
 #pragma unroll
             for (int hh = 0; hh < NH; ++hh)
 #pragma unroll
@@ -638,6 +641,7 @@ __device__ __forceinline__ void decode_split_body(const pa_decode_params& p, int
                     st[hh * HCH + slot]        = kc[s][hh][part];
                     st[(NH + hh) * HCH + slot] = vc[s][hh][part];
                 }
+            wave_lds_sync();   // every lane's rows land before any lane reads its layout
 #pragma unroll
             for (int hh = 0; hh < NH; ++hh) {
 #pragma unroll

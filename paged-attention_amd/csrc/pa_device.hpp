@@ -29,6 +29,18 @@ __device__ __forceinline__ size_t kv_row_offset(int page, int h, int slot, int p
 
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Orders LDS accesses that lanes of one wave use to trade data: every access
+// before the call (e.g. one lane's ds_write) happens before every access after
+// it (another lane's ds_read of the same bytes). LDS runs a wave's operations
+// in issue order, so on gfx950 this emits no instruction; the wavefront-scope
+// fences and the wave barrier keep the compiler from moving LDS accesses
+// across the call.
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 __device__ __forceinline__ float readlane_f(float v, int lane) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
 }

@@ -158,6 +158,8 @@ pa_status pa_cache_append(pa_cache* c, int slot, const uint16_t* d_k, const uint
     return guarded([&] {
         if (!c) throw std::invalid_argument("cache is null");
         if (appended) *appended = 0;
+        if (static_cast<long long>(n) * c->cfg.num_kv_heads * (pa::kHeadDim / 8) > INT_MAX)
+            throw std::length_error("append: n * num_kv_heads * 16 exceeds INT_MAX");
         const int old_len = slot_ok(c->pool, slot) ? c->pool.seq_lens[static_cast<size_t>(slot)] : 0;
         int first_new = 0, num_new = 0;
         if (!pool_reserve(c->pool, slot, n, first_new, num_new)) return;   // out of pages: nothing appended

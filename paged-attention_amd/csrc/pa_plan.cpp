@@ -366,6 +366,9 @@ pa_status pa_append_quantize(int dtype, const uint16_t* k, const uint16_t* v, vo
         if (head_dim != pa::kHeadDim) throw std::invalid_argument("unsupported head_dim " + std::to_string(head_dim));
         if (num_kv_heads <= 0 || page_size <= 0 || start_pos < 0 || n < 0)
             throw std::invalid_argument("append: bad sizes");
+        // One thread per (token, kv head, 8-dim chunk), indexed in 32 bits.
+        if (static_cast<long long>(n) * num_kv_heads * (pa::kHeadDim / 8) > INT_MAX)
+            throw std::length_error("append: n * num_kv_heads * 16 exceeds INT_MAX");
         if (n > 0 && (!k || !v || !k_cache || !v_cache || !block_table_row))
             throw std::invalid_argument("append: null pointer");
         pa::hip_check(pa::launch_append(dtype, k, v, k_cache, v_cache, block_table_row, start_pos, n, num_kv_heads,

@@ -166,10 +166,12 @@ def _append_all(dt, K, V, ck, cv, bt_row, hkv, page_size, inv, fp8):
                   page_size, inv, inv)
 
 
-def paged_inputs(batch, seq_lens, hq, hkv, page_size, fp8, seed):
+def paged_inputs(batch, seq_lens, hq, hkv, page_size, fp8, seed, keep_sources=False):
     """compare_flashinfer.py:80-97 style inputs: N(0,1) pools filled on the
     device, a random page permutation as block table, per-tensor amax/448
-    scales with append-time quantization for FP8."""
+    scales with append-time quantization for FP8. With keep_sources (FP8
+    only) the per-row fp16 sources [L][Hkv][D] of K and V come back as a
+    seventh value, a list of (k, v) device tensors."""
     import torch
     g = torch.Generator(device="cuda").manual_seed(seed)
     pages_per = [math.ceil(L / page_size) for L in seq_lens]
@@ -198,6 +200,8 @@ def paged_inputs(batch, seq_lens, hq, hkv, page_size, fp8, seed):
     iv = float(np.float32(1.0) / np.float32(v_scale))
     for b, (ks, vs) in enumerate(srcs):
         pa_amd.append_quantize(pa_amd.FP8_E4M3, ks, vs, kc, vc, table[b], 0, seq_lens[b], hkv, D, page_size, ik, iv)
+    if keep_sources:
+        return q, kc, vc, table, k_scale, v_scale, srcs
     return q, kc, vc, table, k_scale, v_scale
 
 

@@ -93,3 +93,19 @@ def test_kv_pool_stagger_and_alloc_kv_pools():
         assert k.is_contiguous() and v.is_contiguous()
         assert v.data_ptr() - k.data_ptr() == 3 * 2 * 16 * 128 * elem + gap
         assert k.untyped_storage().data_ptr() == v.untyped_storage().data_ptr()
+
+
+def test_append_rejects_thread_counts_past_int32():
+    """The append kernel indexes (token, kv head, 8-dim chunk) in 32 bits: a
+    single append of n tokens with n * num_kv_heads * 16 > INT_MAX is refused
+    with PA_ERR_LENGTH (std::length_error) before any pointer is used or any
+    kernel is launched; one token fewer than the limit passes the size check
+    and stops at the null-pointer check."""
+    lib = _lib.load()
+    hkv = 8
+    limit = (2**31 - 1) // (hkv * 16)
+    assert lib.pa_append_quantize(1, None, None, None, None, None, 0, limit + 1, hkv, 128, 16, 1.0, 1.0, None) \
+        == _lib.PA_ERR_LENGTH
+    assert b"INT_MAX" in lib.pa_last_error()
+    assert lib.pa_append_quantize(1, None, None, None, None, None, 0, limit, hkv, 128, 16, 1.0, 1.0, None) \
+        == _lib.PA_ERR_INVALID_ARGUMENT

@@ -1,7 +1,9 @@
 """The BASELINE configurations through the torch `Decoder` binding
-(bindings/torch_decode.cu:14-81): C1-C3 and C5 at full size against the
-oracle, C4 at full size with sampled rows, a full-size placement-invariance
-check, and the binding's argument checks.
+(bindings/torch_decode.cu:14-81): C1-C5 at full size against the oracle,
+config 2's page-size sweep at full size (bitwise equal across page sizes, the
+contiguous point against the oracle), config 3's stored FP8 bytes at its own
+amax/448 scales, a full-size placement-invariance check, and the binding's
+argument checks.
 """
 
 from __future__ import annotations
@@ -10,6 +12,7 @@ import numpy as np
 import pytest
 
 import pa_amd
+import oracle
 from helpers import D, TOL, decoder_case, paged_inputs
 
 pytestmark = [pytest.mark.gpu, pytest.mark.usefixtures("gpu_device")]
@@ -37,15 +40,13 @@ def test_decoder_full_size_config3():
     err, _ = decoder_case(64, [8192] * 64, True, threads=16)
     assert err < TOL, err
 
-def test_decoder_full_size_config4_sampled_rows():
+def test_decoder_full_size_config4_all_rows():
     """BASELINE config 4 at full size (128 ragged rows, L ~ U[128, 16384],
-    seed 4) decoded in one batch; 12 rows spread over the batch (first, last,
-    longest, shortest, 8 seeded) checked against the oracle."""
+    seed 4, about 4.3 GB of KV) decoded in one batch; every row against the
+    oracle. Rows split across blocks go through the merge kernel."""
     rng = np.random.default_rng(4)
     lens = [int(x) for x in rng.integers(128, 16385, size=128)]
-    pick = {0, 127, int(np.argmax(lens)), int(np.argmin(lens))}
-    pick |= set(int(x) for x in np.random.default_rng(9).choice(128, 8, replace=False))
-    err, dec = decoder_case(128, lens, False, threads=16, rows=sorted(pick))
+    err, dec = decoder_case(128, lens, False, threads=16)
     assert dec.num_segments >= 128 * 8
     assert err < TOL, err
 
@@ -130,3 +131,91 @@ def test_decoder_rejects_inconsistent_inputs():
         with pytest.raises(RuntimeError):
             dec.run(**{**good, **change})
     torch.cuda.synchronize()
+
+
+def _paged_layout(logical, page_size, perm):
+    """[B][H][L][D] logical K or V -> (pool [B * L / P][H][P][D], table [B][L / P]):
+    logical page i of the batch (row-major over rows, then pages) lives at
+    physical page perm[i]."""
+    import torch
+    B, H, L, Dd = logical.shape
+    npp = L // page_size
+    pages = logical.view(B, H, npp, page_size, Dd).permute(0, 2, 1, 3, 4).reshape(B * npp, H, page_size, Dd)
+    pool = torch.empty_like(pages)
+    pool[perm.long()] = pages
+    return pool, perm.view(B, npp).contiguous()
+
+
+@pytest.mark.parametrize("fp8", DTYPES, ids=IDS)
+def test_full_size_config2_page_size_sweep_bitwise(fp8):
+    """Config 2's page-size sweep at full size (32 x 8192, results/h100_pagesize.csv:2-11,
+    tests/test_paged_decode.cu:171-180): the same q/K/V laid out in pages of
+    4, 8, 16, 32, 64 and 8192 tokens (8192 = one page per sequence, the
+    contiguous point), each under its own seeded page permutation, decode to
+    bitwise the same output (every load path: staged small pages, 16-token
+    runs, whole-sequence pages); the contiguous layout is also checked against
+    the oracle. FP8 uses random finite E4M3 codes at scale 4/448."""
+    import torch
+    B, L, hq, hkv = 32, 8192, 32, 8
+    g = torch.Generator(device="cuda").manual_seed(71)
+    if fp8:
+        def codes():
+            c = torch.randint(0, 0x7f, (B, hkv, L, D), device="cuda", generator=g, dtype=torch.int32).to(torch.uint8)
+            return c | (torch.randint(0, 2, c.shape, device="cuda", generator=g, dtype=torch.int32).to(torch.uint8) << 7)
+        klog, vlog = codes(), codes()
+        ks = vs = 4.0 / 448.0
+    else:
+        klog = torch.randn((B, hkv, L, D), device="cuda", dtype=torch.float16, generator=g)
+        vlog = torch.randn((B, hkv, L, D), device="cuda", dtype=torch.float16, generator=g)
+        ks = vs = 1.0
+    q = torch.randn((B, hq, D), device="cuda", dtype=torch.float16, generator=g)
+    lens = torch.full((B,), L, dtype=torch.int32)
+    outs = {}
+    for P in (4, 8, 16, 32, 64, 8192):
+        perm = torch.randperm(B * (L // P), device="cuda", generator=torch.Generator(device="cuda").manual_seed(P))
+        perm = perm.to(torch.int32)
+        kp, table = _paged_layout(klog, P, perm)
+        vp, _ = _paged_layout(vlog, P, perm)
+        dec = pa_amd.Decoder(hq, hkv, D, P, fp8)
+        dec.plan(lens, 0)
+        outs[P] = dec.run(q, kp, vp, table, lens.cuda(), ks, vs)
+        torch.cuda.synchronize()
+        if P == 8192:
+            dt = pa_amd.FP8_E4M3 if fp8 else pa_amd.FP16
+            kb = kp.cpu().numpy() if fp8 else kp.view(torch.int16).cpu().numpy().view(np.uint16)
+            vb = vp.cpu().numpy() if fp8 else vp.view(torch.int16).cpu().numpy().view(np.uint16)
+            ref = oracle.paged_decode(dt, q.view(torch.int16).cpu().numpy().view(np.uint16), kb, vb,
+                                      table.cpu().numpy(), lens.numpy(), hq, hkv, D, P, ks, vs, threads=16)
+            err = float(np.max(np.abs(outs[P].float().cpu().numpy() - ref)))
+            assert err < TOL, err
+        del kp, vp
+    base = outs[16].view(torch.int16)
+    for P, o in outs.items():
+        assert torch.equal(o.view(torch.int16), base), f"page size {P} differs from 16"
+
+
+def test_full_size_config3_stored_fp8_bytes():
+    """Config 3 at full size (64 x 8192): every FP8 byte the append kernel
+    stored, at the run's own per-tensor scales (amax / 448 over the seeded
+    N(0,1) K and V), equals the oracle's E4M3 store of the same fp16 source
+    (orc_append's encoder, as a 65536-entry table per scale), found through
+    the run's scattered block table."""
+    import torch
+    B, L, hkv, P = 64, 8192, 8, 16
+    q, kc, vc, table, ks, vs, srcs = paged_inputs(B, [L] * B, 32, hkv, P, True, seed=0, keep_sources=True)
+    assert ks > 0 and vs > 0
+    lut_k = oracle.e4m3_quantize_table(float(np.float32(1.0) / np.float32(ks)))
+    lut_v = oracle.e4m3_quantize_table(float(np.float32(1.0) / np.float32(vs)))
+    assert lut_k[0x3c00] != 0                                     # 1.0 quantizes to a nonzero code
+    npp = L // P
+    tab = table.cpu().numpy()
+    pk, pv = kc.cpu().numpy(), vc.cpu().numpy()
+    saturated = 0
+    for b, (ksrc, vsrc) in enumerate(srcs):
+        for src, pool, lut in ((ksrc, pk, lut_k), (vsrc, pv, lut_v)):
+            bits = src.view(torch.int16).cpu().numpy().view(np.uint16)            # [L][Hkv][D]
+            want = lut[bits].reshape(npp, P, hkv, D).transpose(0, 2, 1, 3)        # [page][Hkv][P][D]
+            got = pool[tab[b, :npp]]
+            assert np.array_equal(got, want), f"row {b}: stored FP8 bytes differ"
+            saturated += int(np.count_nonzero((want & 0x7f) == 0x7e))
+    assert saturated >= 2                                          # each tensor's amax lands on +-448

@@ -51,7 +51,7 @@ def test_mixed_length_batch(fp8):
     assert err < TOL, err
 
 @pytest.mark.parametrize("fp8", DTYPES, ids=IDS)
-@pytest.mark.parametrize("page_size", [1, 2, 3, 4, 6, 8, 16, 32, 128])
+@pytest.mark.parametrize("page_size", [1, 2, 3, 4, 6, 8, 16, 32, 128, 256, 8192])
 def test_page_sizes(fp8, page_size):
     err, _, _ = run_cache_case(fp8, 16, 4, page_size, [300, 2500])
     assert err < TOL, err
@@ -84,7 +84,7 @@ def test_output_invariant_under_page_placement(fp8):
     must be bitwise identical across page permutations and page sizes."""
     lens = [700, 1, 2049, 64]
     outs = []
-    for page_size, shuffle in [(16, None), (16, 3), (8, 2), (4, 11), (1, 5), (2048 + 64, None)]:
+    for page_size, shuffle in [(16, None), (16, 3), (8, 2), (4, 11), (1, 5), (2048 + 64, None), (8192, 9)]:
         _, out, _ = run_cache_case(fp8, 32, 8, page_size, lens, shuffle_seed=shuffle)
         outs.append(out)
     for o in outs[1:]:

@@ -108,3 +108,42 @@ def test_paged_decode_matches_float64(fp8, hq, hkv, P):
                               scale, scale, slot_ids=slot_ids, threads=3)
     exp = _numpy_decode(oracle.f16_bits_to_f32(qb), Kq, Vq, lens, hq, hkv)
     assert np.max(np.abs(got - exp)) < 1e-5
+
+
+@pytest.mark.parametrize("use_reference", [False, True], ids=["restatement", "reference"])
+def test_attention_pairs_equal_paged_decode_and_cpu_attention(use_reference):
+    """orc_attention_pairs (the threaded loop the CPU baseline times) computes,
+    for every (row, query head) pair of a ragged GQA batch, bitwise what
+    orc_paged_decode and a direct cpu_attention call compute over the same
+    gathered K/V: the pairs reach the right item (h = hq / G), the right length
+    and the right output row, whatever the thread count."""
+    if use_reference and oracle.ref_lib() is None:
+        pytest.skip("oracle/_ref not built (reference tree absent)")
+    rng = np.random.default_rng(8)
+    hq, hkv, D, P = 16, 4, 128, 16
+    lens = [1, 17, 300, 64, 129]
+    B = len(lens)
+    pages = [-(-L // P) for L in lens]
+    npool = sum(pages) + 2
+    order = rng.permutation(npool).astype(np.int32)
+    table = np.zeros((B, max(pages)), np.int32)
+    off = 0
+    for b, n in enumerate(pages):
+        table[b, :n] = order[off:off + n]
+        off += n
+    kc = oracle.f32_to_f16_bits(rng.standard_normal(npool * hkv * P * D).astype(np.float32))
+    vc = oracle.f32_to_f16_bits(rng.standard_normal(npool * hkv * P * D).astype(np.float32))
+    qb = oracle.f32_to_f16_bits(rng.standard_normal((B, hq, D)).astype(np.float32))
+    ref = oracle.paged_decode(0, qb, kc, vc, table, np.asarray(lens, np.int32), hq, hkv, D, P, threads=3)
+    K = [oracle.gather_dequant(0, kc, table[b], hkv, D, P, h, lens[b]) for b in range(B) for h in range(hkv)]
+    V = [oracle.gather_dequant(0, vc, table[b], hkv, D, P, h, lens[b]) for b in range(B) for h in range(hkv)]
+    qf = oracle.f16_bits_to_f32(qb)
+    for threads in (1, 5):
+        out, secs = oracle.attention_pairs(qf, K, V, lens, hkv, threads=threads, use_reference=use_reference)
+        assert secs >= 0.0
+        assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
+    G = hq // hkv
+    for b in range(B):
+        for h in range(hq):
+            one = oracle.cpu_attention(qf[b, h], K[b * hkv + h // G], V[b * hkv + h // G])
+            assert np.array_equal(one.view(np.uint32), ref[b, h].view(np.uint32))

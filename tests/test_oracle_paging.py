@@ -46,3 +46,24 @@ def test_fp8_append_uses_reciprocal_multiply():
     oracle.append(1, x.reshape(n, 128), x.reshape(n, 128), kc, vc, table, 0, 1, 128, 16, float(inv), float(inv))
     exp = oracle.f32_to_e4m3((xf * inv).astype(np.float32))
     assert np.array_equal(kc[finite], exp[finite])
+
+
+@pytest.mark.parametrize("scale", [1.0, 3.0 / 448.0, 4.0 / 448.0, 4.8125 / 448.0, 5.3271484375 / 448.0, 1e-3])
+def test_e4m3_quantize_table_equals_append(scale):
+    """The quantize table (one byte per fp16 code at a fixed scale) holds, for
+    every one of the 65536 fp16 codes, the byte orc_append stores for that code
+    through its address path (one token row of 128 dims per 128 codes), and
+    the byte of the scalar encoder applied to the fp32 product."""
+    inv = float(np.float32(1.0) / np.float32(scale))
+    table = oracle.e4m3_quantize_table(inv)
+    x = np.arange(65536, dtype=np.uint16)
+    n = 512
+    kc = np.zeros(n * 128, np.uint8)
+    vc = np.zeros_like(kc)
+    pages = np.arange(n // 16, dtype=np.int32)[::-1].copy()     # reversed pages: the scatter matters
+    oracle.append(1, x.reshape(n, 128), x.reshape(n, 128), kc, vc, pages, 0, 1, 128, 16, inv, inv)
+    stored = oracle.gather_raw(1, kc, pages, 1, 128, 16, 0, n).ravel()
+    assert np.array_equal(stored, table)
+    sample = x[::97]
+    prod = (oracle.f16_bits_to_f32(sample) * np.float32(inv)).astype(np.float32)
+    assert np.array_equal(table[sample], oracle.f32_to_e4m3(prod))
