@@ -165,6 +165,22 @@ SIGNATURES: dict[str, tuple] = {
 _lib: ctypes.CDLL | None = None
 
 
+def _init_torch_device_state() -> None:
+    """Lets torch set up its HIP state before this library loads.
+
+    torch and libpa_decode.so share one HIP runtime in a Python process. On
+    the MI355X boxes, when the library was loaded (registering its code
+    objects) before torch's first device query, later HIP calls from one of
+    the two saw no device (hipErrorNoDevice); with torch first, both work. So
+    the library loads only after torch.cuda.is_available() has run (a no-op
+    without a GPU, and when torch is absent)."""
+    try:
+        import torch
+    except ImportError:
+        return
+    torch.cuda.is_available()
+
+
 def load() -> ctypes.CDLL:
     """Loads the library once; raises if it has not been built."""
     global _lib
@@ -174,6 +190,7 @@ def load() -> ctypes.CDLL:
         raise RuntimeError(
             f"{LIB_PATH} is missing: build it with `python paged-attention_amd/build.py` "
             "(or __graft_entry__.build()); there is no fallback path")
+    _init_torch_device_state()
     lib = ctypes.CDLL(str(LIB_PATH))
     for name, (res, args) in SIGNATURES.items():
         fn = getattr(lib, name)
