@@ -152,6 +152,18 @@ pa_status pa_decode(int dtype, const pa_decode_params* p, void* stream);
  * p->needs_merge is 0). pa_decode == pa_decode_split + pa_decode_merge. */
 pa_status pa_decode_split(int dtype, const pa_decode_params* p, void* stream);
 pa_status pa_decode_merge(int dtype, const pa_decode_params* p, void* stream);
+/* No counterpart in the reference. pa_decode for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc): the same split and merge launches, but the partial
+ * workspace of rows split across blocks lives in a fixed 32 MiB device array
+ * of the library (one per GPU, held until the process ends) instead of
+ * p->partial_out / p->partial_lse, which are ignored. num_segments is the
+ * plan's segment count (pa_plan_num_segments); a plan whose workspace,
+ * num_segments * group * (head_dim + 1) * 4 bytes, exceeds 32 MiB is refused
+ * with PA_ERR_LENGTH (plans merged in the split kernel, p->block_merge = 1,
+ * need none). Allocates nothing. Calls on one GPU share its array: calls that
+ * overlap on one GPU (two streams, two threads) race. */
+pa_status pa_decode_static(int dtype, const pa_decode_params* p, int num_segments, void* stream);
 
 /* paged_kv_cache.cu:15-39 quantize<> + append_kernel, launch at :122-131:
  * scatters n tokens of fp16 K/V ([n][num_kv_heads][head_dim]) into pages

@@ -40,7 +40,7 @@ COMMON = [
     f"-I{CSRC}",
 ]
 
-SOURCES = ["pa_decode.hip", "pa_cache.hip", "pa_plan.cpp", "pa_pool.cpp", "pa_kvcache.cpp"]
+SOURCES = ["pa_decode.hip", "pa_cache.hip", "pa_scratch.hip", "pa_plan.cpp", "pa_pool.cpp", "pa_kvcache.cpp"]
 
 
 def _run(cmd: list[str]) -> None:

@@ -124,6 +124,7 @@ SIGNATURES: dict[str, tuple] = {
     "pa_decode": (_I, [_I, ctypes.POINTER(DecodeParams), _P]),
     "pa_decode_split": (_I, [_I, ctypes.POINTER(DecodeParams), _P]),
     "pa_decode_merge": (_I, [_I, ctypes.POINTER(DecodeParams), _P]),
+    "pa_decode_static": (_I, [_I, ctypes.POINTER(DecodeParams), _I, _P]),
     "pa_append_quantize": (_I, [_I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _F, _P]),
     "pa_gather_kv": (_I, [_I, _P, _P, _I, _I, _I, _I, _I, _P, _P]),
     "pa_stream_read": (_I, [_P, _S, _I, _P, _P]),

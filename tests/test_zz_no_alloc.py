@@ -1,0 +1,105 @@
+"""pa_decode_static, the allocation-free variant of pa_decode (no counterpart
+in the reference): the partial workspace of rows split across blocks lives in
+the library's fixed device array instead of the caller's params.
+
+GPU: two calls in a row through the C ABI, the second with a smaller input,
+each bitwise equal to pa_decode on the same plan with the device plan's own
+workspace (same kernels, same arithmetic), and within the tolerance of the
+oracle. CPU: oversized plans and bad arguments are refused before any device
+use.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+
+import oracle
+import pa_amd
+from helpers import D, TOL, paged_inputs
+from pa_amd import _lib
+
+SCRATCH_BYTES = 32 << 20
+
+
+def _params(q, k, v, table, lens, hq, hkv, ks, vs, dplan):
+    import torch
+    p = pa_amd.DecodeParams()
+    p.q, p.k_cache, p.v_cache, p.block_table = q.data_ptr(), k.data_ptr(), v.data_ptr(), table.data_ptr()
+    out = torch.empty_like(q)
+    p.out = out.data_ptr()
+    p.block_table_stride = table.size(1)
+    p.batch, p.num_q_heads, p.num_kv_heads, p.head_dim, p.page_size = len(lens), hq, hkv, D, 16
+    p.sm_scale, p.k_scale, p.v_scale = pa_amd.sm_scale(D), ks, vs
+    dplan.bind(p)
+    return p, out
+
+
+def test_decode_static_refuses_oversized_plans_without_a_device():
+    """A plan whose partial workspace exceeds the 32 MiB array is refused with
+    PA_ERR_LENGTH, and null params, a zero segment count for a non-empty grid,
+    an unknown dtype or an unsupported head_dim with PA_ERR_INVALID_ARGUMENT,
+    before the library looks up the array or launches anything."""
+    lib = _lib.load()
+    p = pa_amd.DecodeParams()
+    p.num_q_heads, p.num_kv_heads, p.head_dim, p.num_ctas, p.batch = 32, 8, D, 2048, 4
+    per_seg = 4 * (D + 1) * 4                         # group 4: 4 rows of head_dim + 1 floats
+    too_many = SCRATCH_BYTES // per_seg + 1
+    assert lib.pa_decode_static(0, ctypes.byref(p), too_many, None) == _lib.PA_ERR_LENGTH
+    assert b"static scratch" in lib.pa_last_error()
+    assert lib.pa_decode_static(0, None, 10, None) == _lib.PA_ERR_INVALID_ARGUMENT
+    assert lib.pa_decode_static(0, ctypes.byref(p), 0, None) == _lib.PA_ERR_INVALID_ARGUMENT
+    assert lib.pa_decode_static(5, ctypes.byref(p), 10, None) == _lib.PA_ERR_INVALID_ARGUMENT
+    p.head_dim = 64
+    assert lib.pa_decode_static(0, ctypes.byref(p), 10, None) == _lib.PA_ERR_INVALID_ARGUMENT
+
+
+@pytest.mark.gpu
+@pytest.mark.usefixtures("gpu_device")
+@pytest.mark.parametrize("fp8", [False, True], ids=["fp16", "fp8"])
+def test_decode_static_matches_decode_on_two_calls(fp8):
+    import torch
+    lib = _lib.load()
+    hq, hkv = 32, 8
+    dt = pa_amd.FP8_E4M3 if fp8 else pa_amd.FP16
+    # Call 1: 4 x 1024 on the default grid (rows split across blocks: merge
+    # kernel). Call 2, smaller: a ragged batch on 100 units. Call 3: 8 x 2048
+    # on 512 units, merged inside the split kernel (no workspace).
+    cases = [([1024] * 4, 0, False), ([700, 33, 2000], 100, False), ([2048] * 8, 512, True)]
+    prev_segments = None
+    for i, (lens, ctas, merged) in enumerate(cases):
+        q, k, v, table, ks, vs = paged_inputs(len(lens), lens, hq, hkv, 16, fp8, seed=40 + i)
+        plan = pa_amd.make_plan(dt, lens, hq, hkv, D, ctas)
+        nseg = len(plan.segments)
+        if prev_segments is not None and not merged:
+            assert nseg < prev_segments                # the second call is the smaller input
+        prev_segments = nseg
+        dplan = pa_amd.DevicePlan()
+        dplan.upload(plan, hq // hkv, D)
+        p_ref, out_ref = _params(q, k, v, table, lens, hq, hkv, ks, vs, dplan)
+        assert (p_ref.block_merge == 1) == merged and (p_ref.needs_merge == 1) == (not merged)
+        p_st, out_st = _params(q, k, v, table, lens, hq, hkv, ks, vs, dplan)
+        p_st.partial_out = None                        # ignored by the static entry point
+        p_st.partial_lse = None
+        out_st.fill_(float("nan"))
+        stream = torch.cuda.current_stream().cuda_stream
+        assert lib.pa_decode(dt, ctypes.byref(p_ref), stream) == _lib.PA_OK
+        assert lib.pa_decode_static(dt, ctypes.byref(p_st), nseg, stream) == _lib.PA_OK, lib.pa_last_error()
+        torch.cuda.synchronize()
+        assert torch.equal(out_st.view(torch.int16), out_ref.view(torch.int16)), f"call {i + 1} differs"
+        if merged:
+            # Merged in LDS: no workspace, so even a segment count past the
+            # array's capacity is accepted.
+            too_many = SCRATCH_BYTES // ((hq // hkv) * (D + 1) * 4) + 1
+            out_st.fill_(float("nan"))
+            assert lib.pa_decode_static(dt, ctypes.byref(p_st), too_many, stream) == _lib.PA_OK
+            torch.cuda.synchronize()
+            assert torch.equal(out_st.view(torch.int16), out_ref.view(torch.int16))
+        kb = k.view(torch.uint8).cpu().numpy() if fp8 else k.view(torch.int16).cpu().numpy().view(np.uint16)
+        vb = v.view(torch.uint8).cpu().numpy() if fp8 else v.view(torch.int16).cpu().numpy().view(np.uint16)
+        ref = oracle.paged_decode(dt, q.view(torch.int16).cpu().numpy().view(np.uint16), kb, vb, table.cpu().numpy(),
+                                  np.asarray(lens, np.int32), hq, hkv, D, 16, ks, vs, threads=16)
+        err = float(np.max(np.abs(out_st.float().cpu().numpy() - ref)))
+        assert err < TOL, (i, err)
