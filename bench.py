@@ -25,10 +25,18 @@ Fields of the JSON line:
   copy_ceiling best plain streaming read of 4 GiB (bench_decode.cu:224-240,
                unrolled / non-temporal variants of it, and the chunked read
                with one contiguous span per wave)
+  workloads    the same figures (step, split kernel, cold) for C1, C3 (the
+               FP8 target), C2 at one page per sequence, C5 fp16 and FP8,
+               timed in the same run; paging_overhead = C2 at 16-token pages
+               against one page per sequence; targets = the goals the
+               north star states, checked on these figures
   cpu_baseline the reference's cpu_attention (compiled from its source into
                oracle/_ref when that exists, else the oracle's restatement)
                over every (row, query head) pair of the same workload, K/V
-               gathered and dequantized to fp32 beforehand (untimed)
+               gathered and dequantized to fp32 beforehand (untimed), on
+               OMP_NUM_THREADS threads (the CPU share of one GPU on the GPU
+               boxes) or every host core; cpu_baseline.c1 times C1 (the
+               reference's CPU-runnable configuration) every run
   roofline.traffic  HBM bytes per split-kernel launch from two rocprofv3
                counter passes run as child processes before this process
                touches the GPU (FETCH_SIZE, then WRITE_SIZE, in KiB per
@@ -119,7 +127,33 @@ def host_fp32_items(s):
     return s.q.float().cpu().numpy(), K, V
 
 
-def cpu_baseline(s, name: str, budget_s: float, threads: int) -> dict:
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_threads(requested: int) -> tuple[int, str]:
+    """Threads for the CPU baseline and why: an explicit --cpu-threads, else
+    OMP_NUM_THREADS (16 on the GPU boxes, the CPU share one GPU is given there,
+    whatever nproc shows), else every core nproc reports."""
+    nproc = os.cpu_count() or 1
+    if requested > 0:
+        return requested, "--cpu-threads"
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    if omp.isdigit() and int(omp) > 0:
+        return min(int(omp), nproc), "OMP_NUM_THREADS (the host's CPU share for this GPU)"
+    return nproc, "nproc (all host cores)"
+
+
+def cpu_time(s, budget_s: float, threads: int, max_runs: int = 3) -> tuple[float, int, bool]:
+    """Median seconds of the CPU attention over every (row, query head) pair
+    of the Setup's workload (K/V gathered and dequantized beforehand, untimed),
+    the number of runs, and whether the reference's compiled cpu_attention ran."""
     import oracle
     q, K, V = host_fp32_items(s)
     use_ref = oracle.ref_lib() is not None
@@ -129,18 +163,33 @@ def cpu_baseline(s, name: str, budget_s: float, threads: int) -> dict:
         _, secs = oracle.attention_pairs(q, K, V, s.lens, HKV, threads=threads, use_reference=use_ref)
         times.append(secs)
         spent = time.perf_counter() - t0
-        if len(times) >= 3 or spent + secs > budget_s:
+        if len(times) >= max_runs or spent + secs > budget_s:
             break
-    med = statistics.median(times)
-    return {
+    return statistics.median(times), len(times), use_ref
+
+
+def cpu_baseline(s, name: str, budget_s: float, threads: int, why: str, c1=None, c1_gpu_us=None) -> dict:
+    med, runs, use_ref = cpu_time(s, budget_s, threads)
+    out = {
         "value": round(s.bytes() / med / 1e9, 3),
         "unit": "GB/s",
         "us_per_step": round(med * 1e6, 1),
         "cores": threads,
+        "cores_source": why,
+        "nproc": os.cpu_count(),
+        "cpu_model": cpu_model(),
         "kind": "reference" if use_ref else "port",
         "sample": (f"all {s.batch * HQ} (row, query head) pairs of {name} ({s.batch} x {max(s.lens)} tokens), "
-                   f"{len(times)} run(s), median; K/V gathered and dequantized to fp32 beforehand (untimed)"),
+                   f"{runs} run(s), median; K/V gathered and dequantized to fp32 beforehand (untimed)"),
     }
+    if c1 is not None:
+        # The reference's CPU-runnable configuration, timed every run beside
+        # the GPU's step on the same inputs.
+        med1, runs1, _ = cpu_time(c1, budget_s, threads, max_runs=20)
+        out["c1"] = {"workload": CONFIGS["c1"][0], "us_per_step": round(med1 * 1e6, 1), "runs": runs1,
+                     "gpu_us_per_step": c1_gpu_us,
+                     "gpu_speedup": round(med1 * 1e6 / c1_gpu_us, 1) if c1_gpu_us else None}
+    return out
 
 
 def time_steps(s, steps: int, warmup: int):
@@ -260,6 +309,32 @@ def device_report() -> dict:
         return {"source": f"amd-smi unavailable ({type(e).__name__})"}
 
 
+# Workloads timed beside the headline one (their figures go under
+# "workloads"): the CPU-runnable C1, the FP8 target C3, the contiguous end of
+# C2's page-size sweep (paging overhead = C2 at 16-token pages against one page
+# per sequence) and C5 in both dtypes. (key, config, page size)
+EXTRA = [("c1", "c1", 16), ("c3", "c3", 16), ("c2_p8192", "c2", 8192), ("c5", "c5", 16), ("c5fp8", "c5fp8", 16)]
+
+
+def workload_figures(s, desc: str, steps: int, warmup: int, cold_iters: int, flusher) -> dict:
+    """One workload's step (K back-to-back steps), split-kernel and cold figures."""
+    wall, split_ms, region_ms = time_steps(s, steps, warmup)
+    nbytes = s.bytes()
+    step_us = wall * 1e6 / steps
+    split_us = (region_ms / steps if s.params.needs_merge == 0 else statistics.mean(split_ms)) * 1e3
+    out = {"workload": desc, "page_size": s.page, "units": s.plan.num_ctas, "segments": int(len(s.plan.segments)),
+           "algorithmic_bytes": nbytes,
+           "us_per_step": round(step_us, 2), "pct_of_peak": round(100 * nbytes / (step_us * 1e-6) / 1e9 / PEAK_GBPS, 2),
+           "split_us": round(split_us, 2),
+           "split_pct_of_peak": round(100 * nbytes / (split_us * 1e-6) / 1e9 / PEAK_GBPS, 2)}
+    if flusher is not None:
+        from pa_amd import bench_decode as bd
+        med = statistics.median(bd.time_cold(flusher, cold_iters, s.run))
+        out["cold_us"] = round(med * 1e3, 2)
+        out["cold_pct_of_peak"] = round(100 * nbytes / (med * 1e-3) / 1e9 / PEAK_GBPS, 2)
+    return out
+
+
 def _barrier() -> None:
     import torch.distributed as dist
     if dist.is_available() and dist.is_initialized():
@@ -276,7 +351,9 @@ def main() -> None:
     ap.add_argument("--ctas", type=int, default=0, help="work units of the plan (0 = one full wave)")
     ap.add_argument("--cold-iters", type=int, default=50)
     ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU-baseline work")
-    ap.add_argument("--cpu-threads", type=int, default=0, help="0 = min(16, host cores)")
+    ap.add_argument("--cpu-threads", type=int, default=0,
+                    help="0 = OMP_NUM_THREADS if set (the box's CPU share), else every host core")
+    ap.add_argument("--no-extra", action="store_true", help="time only the headline workload")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-cold", action="store_true")
     ap.add_argument("--no-copy", action="store_true")
@@ -396,20 +473,54 @@ def main() -> None:
             result["copy_ceiling"]["same_size"] = {
                 "bytes": same["bytes"], "gbps": round(same["gbps"], 1), "frac": round(same["gbps"] / PEAK_GBPS, 4),
                 "kernel": same["kernel"], "time_us": round(same["time_us"], 2)}
-    if not args.no_cold:
-        fl = bd.Flusher()
+    fl = None if args.no_cold else bd.Flusher()
+    if fl is not None:
         cold = bd.time_cold(fl, args.cold_iters, s.run)
         med = statistics.median(cold)
         result["cold"] = {"us_median": round(med * 1e3, 2), "gbps": round(nbytes / (med * 1e-3) / 1e9, 1),
                           "frac": round(nbytes / (med * 1e-3) / 1e9 / PEAK_GBPS, 4),
                           "iters": args.cold_iters, "flush_bytes": fl.buf.numel()}
-        del fl
+
+    # Every setup stays allocated until the end: a timing taken right after a
+    # large free runs a few percent slow while the memory is released.
+    kept = {}
+    if not args.no_extra:
+        result["workloads"] = {}
+        headline = (args.config, args.page_size)
+        for key, cfg, page in EXTRA:
+            if (cfg, page) == headline:
+                continue
+            d = CONFIGS[cfg][0] if page == 16 else f"{CONFIGS[cfg][0].split(',')[0]}, {CONFIGS[cfg][0].split(', ')[1]}, {page}-token pages (one page per sequence)"
+            print(f"# workload {key}: {d}", file=sys.stderr, flush=True)
+            kept[key] = bd.Setup(seq_lens_of(cfg), HQ, HKV, D, page, CONFIGS[cfg][4], shuffle=True, ctas=args.ctas)
+            result["workloads"][key] = workload_figures(kept[key], d, args.steps, args.warmup,
+                                                        min(args.cold_iters, 20), fl)
+        w = result["workloads"]
+        if args.config == "c2" and args.page_size == 16 and "c2_p8192" in w:
+            c = w["c2_p8192"]
+            result["paging_overhead"] = {
+                "page_size": 16, "against_page_size": 8192,
+                "step_pct": round(100 * (result["us_per_step"] / c["us_per_step"] - 1), 2),
+                "split_pct": round(100 * (result["roofline"]["avg_us"] / c["split_us"] - 1), 2),
+                "cold_pct": (round(100 * (result["cold"]["us_median"] / c["cold_us"] - 1), 2)
+                             if "cold" in result and "cold_us" in c else None)}
+        if args.config == "c2" and args.page_size == 16:
+            result["targets"] = {
+                "c2_fp16_step_ge_80pct": result["pct_of_peak"] >= 80.0,
+                "c3_fp8_step_ge_75pct": w["c3"]["pct_of_peak"] >= 75.0 if "c3" in w else None,
+                "paging_overhead_step_lt_2pct": (result["paging_overhead"]["step_pct"] < 2.0
+                                                 if "paging_overhead" in result else None)}
     if not args.no_cpu:
-        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
-        result["cpu_baseline"] = cpu_baseline(s, args.config, args.cpu_budget, threads)
+        threads, why = cpu_threads(args.cpu_threads)
+        c1 = kept.get("c1")
+        c1_gpu = result["workloads"]["c1"]["us_per_step"] if c1 is not None else None
+        result["cpu_baseline"] = cpu_baseline(s, args.config, args.cpu_budget, threads, why, c1, c1_gpu)
 
     result["device"] = device
+    for k in kept.values():
+        k.close()
     s.close()
+    del fl
     print(json.dumps(result), flush=True)
 
 
