@@ -11,7 +11,7 @@
 //   bench_decode single    --batch B --len L     one configuration
 //
 // Common flags: --hq 32 --hkv 8 --dim 128 --page 16 --iters 50 --dtype fp16|fp8
-//               --ctas N (0 = default grid) --contiguous-pages --peak-gbps X (8000)
+//               --ctas N (0 = default grid) --contiguous-pages --peak-gbps X|device (8000)
 //
 // Timing (bench_decode.cu:120-139): the step is planned once; each iteration
 // streams a 1 GiB buffer first (more than L2 plus the 256 MiB Infinity Cache),
@@ -30,8 +30,10 @@
 #include <cstdint>
 #include <cstdio>
 #include <cstdlib>
+#include <cerrno>
+#include <climits>
 #include <cstring>
-#include <map>
+#include <iterator>
 #include <memory>
 #include <stdexcept>
 #include <string>
@@ -74,34 +76,109 @@ __global__ void abs_max_f16(const __half* x, size_t n, unsigned int* amax) {
 }
 
 // ---- command line -------------------------------------------------------------
+// Every option is a typed field with its default. "--name value" and
+// "--name=value" both work; switches take no value. An unknown option, a
+// missing or malformed value, or a stray argument is an error: the usage goes
+// to stderr and the CLI exits with status 2.
 
-struct Args {
+struct Options {
     std::string mode = "sweep";
-    std::map<std::string, std::string> kv;
-    bool has(const std::string& k) const { return kv.count(k) != 0; }
-    int i(const std::string& k, int d) const { return has(k) ? std::atoi(kv.at(k).c_str()) : d; }
-    double f(const std::string& k, double d) const { return has(k) ? std::atof(kv.at(k).c_str()) : d; }
-    std::string s(const std::string& k, const std::string& d) const { return has(k) ? kv.at(k) : d; }
+    int batch = 32, len = 4096, hq = 32, hkv = 8, dim = 128, page = 16, iters = 50, ctas = 0, max_len = 8192;
+    double budget_gib = 1.0;
+    std::string dtype;           // "" = both dtypes in sweep, fp16 elsewhere
+    std::string peak = "8000";   // GB/s, or "device": memory clock x bus width
+    bool contiguous_pages = false;
+    bool help = false;
 };
 
-Args parse_args(int argc, char** argv) {
-    Args a;
-    int at = 1;
-    if (argc > 1 && std::strncmp(argv[1], "--", 2) != 0) a.mode = argv[at++];
-    while (at < argc) {
-        std::string key = argv[at++];
-        if (key.rfind("--", 0) != 0) continue;
-        key.erase(0, 2);
-        const bool has_value = at < argc && std::strncmp(argv[at], "--", 2) != 0;
-        a.kv[key] = has_value ? argv[at++] : "1";
+struct OptionSpec {
+    const char* name;
+    enum Kind { Int, Real, Text, Switch } kind;
+    void* field;
+};
+
+std::vector<OptionSpec> option_specs(Options& o) {
+    return {{"batch", OptionSpec::Int, &o.batch},          {"len", OptionSpec::Int, &o.len},
+            {"hq", OptionSpec::Int, &o.hq},                {"hkv", OptionSpec::Int, &o.hkv},
+            {"dim", OptionSpec::Int, &o.dim},              {"page", OptionSpec::Int, &o.page},
+            {"iters", OptionSpec::Int, &o.iters},          {"ctas", OptionSpec::Int, &o.ctas},
+            {"max-len", OptionSpec::Int, &o.max_len},      {"budget-gib", OptionSpec::Real, &o.budget_gib},
+            {"dtype", OptionSpec::Text, &o.dtype},         {"peak-gbps", OptionSpec::Text, &o.peak},
+            {"contiguous-pages", OptionSpec::Switch, &o.contiguous_pages},
+            {"help", OptionSpec::Switch, &o.help}};
+}
+
+// Fills `o` from argv; on a bad command line returns false with `err` set.
+bool parse_options(int argc, char** argv, Options& o, std::string& err) {
+    const std::vector<OptionSpec> specs = option_specs(o);
+    for (int at = 1; at < argc; ++at) {
+        const std::string arg = argv[at];
+        if (arg == "-h") {
+            o.help = true;
+            continue;
+        }
+        if (arg.size() < 3 || arg.compare(0, 2, "--") != 0) {
+            if (at != 1) {
+                err = "unexpected argument '" + arg + "'";
+                return false;
+            }
+            o.mode = arg;   // the mode comes first
+            continue;
+        }
+        const size_t eq = arg.find('=');
+        const std::string name = arg.substr(2, eq == std::string::npos ? std::string::npos : eq - 2);
+        const auto spec = std::find_if(specs.begin(), specs.end(), [&](const OptionSpec& x) { return name == x.name; });
+        if (spec == specs.end()) {
+            err = "unknown option --" + name;
+            return false;
+        }
+        if (spec->kind == OptionSpec::Switch) {
+            if (eq != std::string::npos) {
+                err = "--" + name + " takes no value";
+                return false;
+            }
+            *static_cast<bool*>(spec->field) = true;
+            continue;
+        }
+        std::string value;
+        if (eq != std::string::npos) value = arg.substr(eq + 1);
+        else if (at + 1 < argc) value = argv[++at];
+        else {
+            err = "--" + name + " needs a value";
+            return false;
+        }
+        char* rest = nullptr;
+        errno = 0;
+        if (spec->kind == OptionSpec::Int) {
+            const long x = std::strtol(value.c_str(), &rest, 10);
+            if (errno || rest == value.c_str() || *rest || x < INT_MIN || x > INT_MAX) {
+                err = "--" + name + " needs an integer, got '" + value + "'";
+                return false;
+            }
+            *static_cast<int*>(spec->field) = static_cast<int>(x);
+        } else if (spec->kind == OptionSpec::Real) {
+            const double x = std::strtod(value.c_str(), &rest);
+            if (errno || rest == value.c_str() || *rest) {
+                err = "--" + name + " needs a number, got '" + value + "'";
+                return false;
+            }
+            *static_cast<double*>(spec->field) = x;
+        } else {
+            *static_cast<std::string*>(spec->field) = value;
+        }
     }
-    return a;
+    if (!o.dtype.empty() && o.dtype != "fp16" && o.dtype != "fp8") {
+        err = "--dtype must be fp16 or fp8";
+        return false;
+    }
+    return true;
 }
 
 const char* kUsage =
     "usage: bench_decode sweep|ctas|pagesize|capacity|copy|single [--batch B] [--len L] [--dtype fp16|fp8]\n"
     "       [--hq 32] [--hkv 8] [--dim 128] [--page 16] [--iters 50] [--ctas 0] [--contiguous-pages]\n"
-    "       [--budget-gib 1] [--max-len 8192] [--peak-gbps 8000]\n";
+    "       [--budget-gib 1] [--max-len 8192] [--peak-gbps 8000|device]\n"
+    "  --peak-gbps device: the device's memory clock x bus width x 2 (double data rate)\n";
 
 // ---- timing -----------------------------------------------------------------
 
@@ -256,7 +333,7 @@ void run_one(const Gpu& g, const Flusher& fl, Setup& s, int ctas, int iters) {
     std::fflush(stdout);
 }
 
-int run(const Args& a) {
+int run(const Options& a) {
     Gpu g;
     {
         hipDeviceProp_t prop;
@@ -270,14 +347,30 @@ int run(const Args& a) {
             g.name = "AMD " + arch.substr(0, arch.find(':'));
         }
         std::replace(g.name.begin(), g.name.end(), ',', ' ');
-        g.cus  = prop.multiProcessorCount;
-        g.peak = a.f("peak-gbps", 8000.0);
+        g.cus = prop.multiProcessorCount;
+        // The DRAM peak the device reports (bench_decode.cu:87-100 derives it
+        // the same way): memory clock (kHz) x bus width (bits) / 8 x 2.
+        int clock_khz = 0, bus_bits = 0;
+        if (hipDeviceGetAttribute(&clock_khz, hipDeviceAttributeMemoryClockRate, dev) != hipSuccess) clock_khz = 0;
+        if (hipDeviceGetAttribute(&bus_bits, hipDeviceAttributeMemoryBusWidth, dev) != hipSuccess) bus_bits = 0;
+        const double device_peak = 2.0 * clock_khz * 1e3 * (bus_bits / 8.0) / 1e9;
+        std::fprintf(stderr, "# device-reported DRAM peak: %.0f GB/s (memory clock %d kHz, bus %d bits)\n",
+                     device_peak, clock_khz, bus_bits);
+        if (a.peak == "device") {
+            if (device_peak <= 0) throw std::runtime_error("the device reports no memory clock or bus width");
+            g.peak = device_peak;
+        } else {
+            char* rest = nullptr;
+            g.peak = std::strtod(a.peak.c_str(), &rest);
+            if (rest == a.peak.c_str() || *rest || g.peak <= 0)
+                throw std::invalid_argument("--peak-gbps needs a positive number or 'device'");
+        }
     }
     std::fprintf(stderr, "# %s, %d CUs, HBM peak %.0f GB/s\n", g.name.c_str(), g.cus, g.peak);
-    const int hq = a.i("hq", 32), hkv = a.i("hkv", 8), dim = a.i("dim", 128);
-    const int page = a.i("page", 16), iters = a.i("iters", 50), ctas = a.i("ctas", 0);
-    const bool shuffle = !a.has("contiguous-pages");
-    const decode::KVDtype dt = a.s("dtype", "fp16") == "fp8" ? decode::KVDtype::FP8_E4M3 : decode::KVDtype::FP16;
+    const int hq = a.hq, hkv = a.hkv, dim = a.dim;
+    const int page = a.page, iters = a.iters, ctas = a.ctas;
+    const bool shuffle = !a.contiguous_pages;
+    const decode::KVDtype dt = a.dtype == "fp8" ? decode::KVDtype::FP8_E4M3 : decode::KVDtype::FP16;
 
     if (a.mode == "copy") {   // bench_decode.cu:224-240 plus the chunked read
         const size_t bytes = size_t{4} << 30;
@@ -312,8 +405,8 @@ int run(const Args& a) {
         return 0;
     }
     if (a.mode == "capacity") {   // bench_decode.cu:285-321 through the host allocator
-        const size_t budget = static_cast<size_t>(a.f("budget-gib", 1.0) * static_cast<double>(size_t{1} << 30));
-        const int max_len = a.i("max-len", 8192);
+        const size_t budget = static_cast<size_t>(a.budget_gib * static_cast<double>(size_t{1} << 30));
+        const int max_len = a.max_len;
         const int per_slot = (max_len + page - 1) / page;
         std::printf("dtype,layout,max_len,actual_len,sequences,bytes_per_seq\n");
         for (int actual : {256, 512, 1024, 2048, 4096, 8192}) {
@@ -348,11 +441,11 @@ int run(const Args& a) {
     }
 
     Flusher fl;
-    const int batch = a.i("batch", 32), len = a.i("len", 4096);
+    const int batch = a.batch, len = a.len;
     if (a.mode == "sweep") {
         std::printf("%s\n", kHeader);
         std::vector<decode::KVDtype> dts;
-        if (a.has("dtype")) dts = {dt};
+        if (!a.dtype.empty()) dts = {dt};
         else dts = {decode::KVDtype::FP16, decode::KVDtype::FP8_E4M3};
         const std::vector<std::pair<int, int>> shapes = {{1, 4096},  {1, 16384}, {1, 65536}, {1, 131072},
                                                          {8, 4096},  {8, 16384}, {8, 32768}, {32, 1024},
@@ -401,10 +494,20 @@ int run(const Args& a) {
 }  // namespace
 
 int main(int argc, char** argv) {
-    const Args a = parse_args(argc, argv);
-    if (a.has("help") || a.mode == "help") {   // no device use
+    Options a;
+    std::string err;
+    if (!parse_options(argc, argv, a, err)) {   // no device use
+        std::fprintf(stderr, "bench_decode: %s\n%s", err.c_str(), kUsage);
+        return 2;
+    }
+    if (a.help || a.mode == "help") {
         std::fputs(kUsage, stdout);
         return 0;
+    }
+    static const char* const kModes[] = {"sweep", "ctas", "pagesize", "capacity", "copy", "single"};
+    if (std::none_of(std::begin(kModes), std::end(kModes), [&](const char* m) { return a.mode == m; })) {
+        std::fprintf(stderr, "bench_decode: unknown mode %s\n%s", a.mode.c_str(), kUsage);
+        return 2;
     }
     try {
         return run(a);

@@ -339,23 +339,23 @@ def append_rows(batch: int, hkv: int, dim: int, page: int, fp8: bool, steps: int
     return rows
 
 
-def _parse(argv: list[str]):
-    mode = "sweep"
-    kv: dict[str, str] = {}
-    i = 0
-    if argv and not argv[0].startswith("-"):
-        mode = argv[0]
-        i = 1
-    while i < len(argv):
-        k = argv[i]
-        if k.startswith("--"):
-            if i + 1 < len(argv) and not argv[i + 1].startswith("--"):
-                kv[k[2:]] = argv[i + 1]
-                i += 1
-            else:
-                kv[k[2:]] = "1"
-        i += 1
-    return mode, kv
+def _options(argv: list[str]):
+    """The command line as typed options (argparse: unknown options, bad values
+    and unknown modes exit with status 2; --help prints the usage). No device
+    is touched before it succeeds."""
+    import argparse
+    ap = argparse.ArgumentParser(prog="python -m pa_amd.bench_decode", description=__doc__,
+                                 formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("mode", nargs="?", default="sweep", choices=MODES)
+    for name, default in (("batch", None), ("len", None), ("hq", 32), ("hkv", 8), ("dim", 128), ("page", 16),
+                          ("iters", 50), ("ctas", 0), ("steps", 200), ("max-len", 8192)):
+        ap.add_argument(f"--{name}", type=int, default=default)
+    ap.add_argument("--dtype", choices=("fp16", "fp8"), default=None)
+    ap.add_argument("--budget-gib", type=float, default=1.0)
+    ap.add_argument("--peak-gbps", type=float, default=PEAK_GBPS)
+    ap.add_argument("--contiguous-pages", action="store_true", help="no free-list shuffle")
+    ap.add_argument("--warm", action="store_true", help="no cache flush between iterations")
+    return ap.parse_args(argv)
 
 
 def run_one(gpu: str, peak: float, fl: Flusher | None, s: Setup, ctas: int, iters: int) -> dict:
@@ -374,23 +374,18 @@ MODES = ("sweep", "ctas", "pagesize", "capacity", "copy", "single", "append")
 
 
 def main(argv: list[str] | None = None) -> int:
-    args = sys.argv[1:] if argv is None else argv
-    mode, a = _parse(args)
-    if "help" in a or "h" in a or "-h" in args or mode not in MODES:
-        # Usage needs no device (the reference prints it before touching CUDA).
-        print(__doc__, file=sys.stdout if mode in MODES else sys.stderr)
-        return 0 if mode in MODES else 2
+    o = _options(sys.argv[1:] if argv is None else argv)
+    mode = o.mode
     import torch
-    geti = lambda k, d: int(a.get(k, d))   # noqa: E731
     core.load()
     props = torch.cuda.get_device_properties(0)
     gpu = gpu_name()
     cus = props.multi_processor_count
-    peak = float(a.get("peak-gbps", PEAK_GBPS))
+    peak = o.peak_gbps
     print(f"# {gpu}, {cus} CUs, HBM peak {peak:.0f} GB/s", file=sys.stderr, flush=True)
-    hq, hkv, dim = geti("hq", 32), geti("hkv", 8), geti("dim", 128)
-    page, iters, ctas = geti("page", 16), geti("iters", 50), geti("ctas", 0)
-    shuffle = "contiguous-pages" not in a
+    hq, hkv, dim = o.hq, o.hkv, o.dim
+    page, iters, ctas = o.page, o.iters, o.ctas
+    shuffle = not o.contiguous_pages
 
     if mode == "copy":
         print("gpu,kernel,bytes,time_us,gbps,pct_peak")
@@ -399,16 +394,16 @@ def main(argv: list[str] | None = None) -> int:
                   f"{100 * r['gbps'] / peak:.1f}", flush=True)
         return 0
 
-    fp8 = a.get("dtype", "fp16") == "fp8"
+    fp8 = o.dtype == "fp8"
     if mode == "append":
         print("gpu,dtype,mode,batch,tokens_per_seq,calls_per_step,us_per_step,gbps,pct_peak")
-        b = geti("batch", 64)
-        for r in append_rows(b, hkv, dim, page, fp8, geti("steps", 200), geti("len", 1024)):
+        b = o.batch if o.batch is not None else 64
+        for r in append_rows(b, hkv, dim, page, fp8, o.steps, o.len if o.len is not None else 1024):
             print(f"{gpu},{'fp8_e4m3' if fp8 else 'fp16'},{r['mode']},{b},{r['tokens']},{r['calls']},"
                   f"{r['us']:.2f},{r['gbps']:.1f},{100 * r['gbps'] / peak:.1f}", flush=True)
         return 0
 
-    fl = None if "warm" in a else Flusher()
+    fl = None if o.warm else Flusher()
     # Multi-row modes keep every row's cache until the mode ends: a row timed
     # within some milliseconds of freeing an earlier row's cache ran about 5%
     # slower (32 x 8192 fp16: 170.8 against 161.7 us) while the freed memory
@@ -416,7 +411,7 @@ def main(argv: list[str] | None = None) -> int:
     kept: list[Setup] = []
     if mode == "sweep":
         print(HEADER)
-        dts = [fp8] if "dtype" in a else [False, True]
+        dts = [fp8] if o.dtype else [False, True]
         for dt in dts:
             for b, L in SWEEP_SHAPES:
                 kept.append(Setup([L] * b, hq, hkv, dim, page, dt, shuffle))
@@ -425,7 +420,8 @@ def main(argv: list[str] | None = None) -> int:
             s.close()
         return 0
 
-    batch, length = geti("batch", 32), geti("len", 4096)
+    batch = o.batch if o.batch is not None else 32
+    length = o.len if o.len is not None else 4096
     if mode == "single":
         print(HEADER)
         s = Setup([length] * batch, hq, hkv, dim, page, fp8, shuffle)
@@ -452,8 +448,8 @@ def main(argv: list[str] | None = None) -> int:
         return 0
     if mode == "capacity":
         # bench_decode.cu:285-321: sequences that fit one layer's KV budget.
-        budget = int(float(a.get("budget-gib", 1.0)) * (1 << 30))
-        max_len = geti("max-len", 8192)
+        budget = int(o.budget_gib * (1 << 30))
+        max_len = o.max_len
         print("dtype,layout,max_len,actual_len,sequences,bytes_per_seq")
         for actual in (256, 512, 1024, 2048, 4096, 8192):
             per_contig = 2 * max_len * hkv * dim * 2
@@ -475,8 +471,7 @@ def main(argv: list[str] | None = None) -> int:
                       f"{cache.total_bytes() // n if n else 0}", flush=True)
                 cache.close()
         return 0
-    print(f"unknown mode {mode}", file=sys.stderr)
-    return 1
+    raise AssertionError(f"mode {mode} has no handler")
 
 
 if __name__ == "__main__":

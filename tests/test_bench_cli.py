@@ -72,3 +72,16 @@ def test_python_twin_help_needs_no_device():
     r = subprocess.run([sys.executable, "-m", "pa_amd.bench_decode", "nosuchmode"], capture_output=True, text=True,
                        timeout=120, cwd=cwd)
     assert r.returncode == 2
+
+
+def test_bad_command_lines_exit_2_without_a_device():
+    """Unknown options, malformed or missing values, stray arguments, an
+    unknown dtype or mode: the usage goes to stderr and the CLI exits with 2
+    before it touches a device."""
+    for args in (["single", "--bogus"], ["single", "--batch", "x"], ["ctas", "--batch"], ["single", "extra"],
+                 ["single", "--dtype", "fp9"], ["nosuchmode"], ["single", "--contiguous-pages=1"]):
+        proc = subprocess.run([str(_bin()), *args], capture_output=True, text=True, timeout=60)
+        assert proc.returncode == 2, (args, proc.stdout, proc.stderr)
+        assert "usage: bench_decode" in proc.stderr
+    out = _run("--help", "--batch=3")
+    assert out.startswith("usage: bench_decode")
