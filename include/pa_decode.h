@@ -135,7 +135,12 @@ pa_status pa_device_plan_create(pa_device_plan** out);
 void      pa_device_plan_destroy(pa_device_plan* dp);
 /* decode.cu:131-146 DevicePlan::upload: grow-only device copies of the plan plus
  * the partial workspace (segments * group * (head_dim + 1) floats). Rejects a
- * plan whose segments do not start on multiples of 16 tokens. */
+ * plan whose segments do not start on multiples of 16 tokens. The plan's arrays
+ * go through pinned staging as one copy queued on `stream`; the call does not
+ * synchronize the stream (it waits only when 8 of its uploads are still in
+ * flight, and synchronizes once when a plan outgrows every earlier one), and
+ * the host plan may change or go as soon as it returns. Decodes queued earlier
+ * on `stream` still see the previous plan. */
 pa_status pa_device_plan_upload(pa_device_plan* dp, const pa_plan* plan, int group, int head_dim,
                                 void* stream);
 /* decode.cu:148-156 DevicePlan::bind: points the schedule fields of *p at it. */
@@ -284,14 +289,15 @@ pa_status pa_cache_append(pa_cache* cache, int slot, const uint16_t* d_k, const 
  * block-table entries and lengths go over in one pinned host-to-device copy and
  * one kernel writes them together with every token (copy or E4M3 quantize): two
  * stream operations, no stream synchronization. The call returns once its host
- * staging is queued; it waits only for the batch before the previous one. */
+ * staging is queued; it waits only when 8 of its batches are still in flight. */
 pa_status pa_cache_append_batch(pa_cache* cache, const int32_t* slots, const int32_t* counts, int n,
                                 const uint16_t* d_k, const uint16_t* d_v, void* stream, int* appended);
 pa_status pa_cache_release(pa_cache* cache, int slot);
 void      pa_cache_shuffle_free_pages(pa_cache* cache, unsigned seed);
 /* paged_kv_cache.cu:157-171 params(): cache-side fields of DecodeParams. */
 pa_status pa_cache_params(const pa_cache* cache, pa_decode_params* p);
-/* paged_kv_cache.cu:173-191 plan(slots, num_q_heads, num_ctas). */
+/* paged_kv_cache.cu:173-191 plan(slots, num_q_heads, num_ctas). Queues the plan
+ * and the slot ids like pa_device_plan_upload: no stream synchronization. */
 pa_status pa_cache_plan(pa_cache* cache, const int32_t* slots, int n, int num_q_heads,
                         int num_ctas, void* stream);
 /* paged_kv_cache.cu:193-202 run(q, out). */

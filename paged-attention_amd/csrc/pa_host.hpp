@@ -25,18 +25,44 @@ struct pa_plan {
     std::vector<int32_t> item_seg_begin;  // [items + 1]
 };
 
-// Device copy of a plan plus the partial workspace (decode.hpp:44-63).
+// One pinned host staging buffer for host-to-device copies on a stream: pinned
+// host ints, optionally their own device copy, and an event recorded after the
+// last stream operation that reads them.
+struct pa_stage {
+    int32_t*   host = nullptr;
+    int32_t*   dev  = nullptr;
+    size_t     cap  = 0;   // int32 elements
+    hipEvent_t done = nullptr;
+};
+
+// Staging buffers for copies that may still be in flight while the next one is
+// staged: a call takes any buffer whose last copy has finished and adds a buffer
+// (up to kMaxStages) when none has, so a caller that runs a few steps ahead of
+// the device never waits for it.
+struct pa_stage_pool {
+    static constexpr size_t kMaxStages = 8;
+    std::vector<pa_stage> bufs;
+    size_t next = 0;   // where the search for a finished buffer starts
+};
+
+// Device copy of a plan plus the partial workspace (decode.hpp:44-63). The
+// plan's int arrays share one device block: segments, cta_seg_begin,
+// item_seg_begin, then the caller's extra ints (the cache's slot ids).
 struct pa_device_plan {
+    int32_t* ints           = nullptr;   // the block
+    size_t   ints_cap       = 0;         // int32 elements
     int32_t* segments       = nullptr;
     int32_t* cta_seg_begin  = nullptr;
     int32_t* item_seg_begin = nullptr;
+    int32_t* extra          = nullptr;
     float*   partial_out    = nullptr;
     float*   partial_lse    = nullptr;
-    size_t   seg_cap = 0, cta_cap = 0, item_cap = 0, part_cap = 0;
+    size_t   part_cap = 0;
     int      num_ctas    = 0;
     int      needs_merge = 0;
     int      max_item_segments = 0;
     bool     block_merge = false;
+    pa_stage_pool staging;
 };
 
 // Host page allocator and per-slot block tables (paged_kv_cache.hpp:89-92).
@@ -50,15 +76,6 @@ struct pa_pool {
     std::vector<char>                 occupied;
 };
 
-// One host-to-device staging buffer of the batched append: pinned host ints,
-// their device copy, and an event recorded after the kernel that reads them.
-struct pa_stage {
-    int32_t*   host = nullptr;
-    int32_t*   dev  = nullptr;
-    size_t     cap  = 0;   // int32 elements
-    hipEvent_t done = nullptr;
-};
-
 struct pa_cache {
     pa_cache_config cfg{};
     pa_pool         pool;
@@ -66,14 +83,11 @@ struct pa_cache {
     void*           d_v          = nullptr;
     int32_t*        d_table      = nullptr;   // [max_slots][max_pages_per_slot]
     int32_t*        d_seq_lens   = nullptr;   // [max_slots]
-    int32_t*        d_slot_ids   = nullptr;
-    size_t          slot_ids_cap = 0;
     pa_plan         plan;
-    pa_device_plan  dplan;
+    pa_device_plan  dplan;                    // its extra ints are the plan's slot ids
     int             plan_batch = 0;
     int             plan_hq    = 0;
-    pa_stage        stage[2];   // used in turn, so one batch may still be in flight while the next is staged
-    int             stage_next = 0;
+    pa_stage_pool   append_staging;           // the batched append's metadata
 };
 
 namespace pa::host {
@@ -108,23 +122,26 @@ inline pa_status guarded(F&& f) {
 
 inline hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
 
-// Grow-only device buffer refreshed from host data on `s`.
-template <class T>
-inline void upload_grow(T*& dst, size_t& cap, const T* src, size_t n, hipStream_t s) {
-    if (n > cap) {
-        pa::hip_check(hipFree(dst), "hipFree");
-        dst = nullptr;
-        pa::hip_check(hipMalloc(reinterpret_cast<void**>(&dst), sizeof(T) * n), "hipMalloc");
-        cap = n;
-    }
-    if (n) pa::hip_check(hipMemcpyAsync(dst, src, sizeof(T) * n, hipMemcpyHostToDevice, s), "hipMemcpyAsync");
-}
+// ---- staging (pa_plan.cpp)
+// A buffer of the pool with room for `need` ints (and a device copy of that
+// size when with_device) whose last use has finished: a free one, else a new
+// one, else (kMaxStages in flight) the oldest after waiting for it. Grows a
+// buffer by reallocating. The reference is valid until the next take_stage.
+pa_stage& take_stage(pa_stage_pool& sp, size_t need, bool with_device);
+// Records the buffer's event on s: call after queuing the work that reads it.
+void release_stage(pa_stage& st, hipStream_t s);
+// Waits for every queued use of the pool and frees its buffers and events.
+void free_stages(pa_stage_pool& sp);
 
 // ---- planner and device plan (pa_plan.cpp)
 void check_dtype(int dtype);
 void make_plan_impl(pa_plan& plan, int dtype, const int32_t* lens, int batch, int hq, int hkv, int hd,
                     int num_ctas);
-void device_plan_upload(pa_device_plan& dp, const pa_plan& plan, int group, int head_dim, hipStream_t s);
+// Queues the plan's arrays (and n_extra caller ints, kept at dp.extra) for the
+// device on s through pinned staging and returns: no stream synchronization.
+// The host plan may change or go right after the call.
+void device_plan_upload(pa_device_plan& dp, const pa_plan& plan, int group, int head_dim, hipStream_t s,
+                        const int32_t* extra = nullptr, size_t n_extra = 0);
 void device_plan_bind(const pa_device_plan& dp, pa_decode_params& p);
 void device_plan_free(pa_device_plan& dp);
 void decode_impl(int dtype, const pa_decode_params& p, hipStream_t s, bool split, bool merge);

@@ -44,9 +44,7 @@ void cache_plan(pa_cache& c, const int32_t* slots, int n, int hq, int num_ctas, 
         lens[static_cast<size_t>(i)] = c.pool.seq_lens[static_cast<size_t>(slots[i])];
     }
     make_plan_impl(c.plan, c.cfg.dtype, lens.data(), n, hq, c.cfg.num_kv_heads, c.cfg.head_dim, num_ctas);
-    device_plan_upload(c.dplan, c.plan, hq / c.cfg.num_kv_heads, c.cfg.head_dim, s);
-    upload_grow(c.d_slot_ids, c.slot_ids_cap, slots, static_cast<size_t>(n), s);
-    pa::hip_check(hipStreamSynchronize(s), "hipStreamSynchronize");
+    device_plan_upload(c.dplan, c.plan, hq / c.cfg.num_kv_heads, c.cfg.head_dim, s, slots, static_cast<size_t>(n));
     c.plan_batch = n;
     c.plan_hq    = hq;
 }
@@ -56,33 +54,11 @@ void cache_run(pa_cache& c, const uint16_t* q, uint16_t* out, hipStream_t s) {
     cache_params(c, p);
     p.q           = q;
     p.out         = out;
-    p.slot_ids    = c.d_slot_ids;
+    p.slot_ids    = c.dplan.extra;
     p.batch       = c.plan_batch;
     p.num_q_heads = c.plan_hq;
     device_plan_bind(c.dplan, p);
     decode_impl(c.cfg.dtype, p, s, true, true);
-}
-
-// Takes the next staging buffer with room for `need` ints, waiting for the
-// batch that last used it (its copy and kernel) to finish.
-pa_stage& take_stage(pa_cache& c, size_t need) {
-    pa_stage& st = c.stage[c.stage_next];
-    c.stage_next ^= 1;
-    if (!st.done) pa::hip_check(hipEventCreateWithFlags(&st.done, hipEventDisableTiming), "hipEventCreate");
-    pa::hip_check(hipEventSynchronize(st.done), "hipEventSynchronize staging");
-    if (st.cap < need) {
-        const size_t cap = std::max<size_t>(need + need / 2, 4096);
-        (void)hipHostFree(st.host);
-        (void)hipFree(st.dev);
-        st.host = nullptr;
-        st.dev  = nullptr;
-        st.cap  = 0;
-        pa::hip_check(hipHostMalloc(reinterpret_cast<void**>(&st.host), cap * sizeof(int32_t), hipHostMallocDefault),
-                      "hipHostMalloc staging");
-        pa::hip_check(hipMalloc(reinterpret_cast<void**>(&st.dev), cap * sizeof(int32_t)), "hipMalloc staging");
-        st.cap = cap;
-    }
-    return st;
 }
 
 }  // namespace
@@ -139,13 +115,7 @@ void pa_cache_destroy(pa_cache* c) {
     (void)hipFree(c->d_k);   // both pools
     (void)hipFree(c->d_table);
     (void)hipFree(c->d_seq_lens);
-    (void)hipFree(c->d_slot_ids);
-    for (pa_stage& st : c->stage) {
-        if (st.done) (void)hipEventSynchronize(st.done);
-        (void)hipHostFree(st.host);
-        (void)hipFree(st.dev);
-        if (st.done) (void)hipEventDestroy(st.done);
-    }
+    free_stages(c->append_staging);
     device_plan_free(c->dplan);
     delete c;
 }
@@ -216,7 +186,7 @@ pa_status pa_cache_append_batch(pa_cache* c, const int32_t* slots, const int32_t
         for (int i = 0; i < n; ++i)
             if (!seen[static_cast<size_t>(slots[i])]) seen[static_cast<size_t>(slots[i])] = 1, ++n_len;
         const size_t need = 3 * static_cast<size_t>(n) + static_cast<size_t>(n_pl) + 2 * static_cast<size_t>(n_tab + n_len);
-        pa_stage& st = take_stage(*c, need);
+        pa_stage& st = take_stage(c->append_staging, need, true);
         int32_t* tok_begin = st.host;
         int32_t* old_len   = tok_begin + n;
         int32_t* pl_begin  = old_len + n;
@@ -268,7 +238,7 @@ pa_status pa_cache_append_batch(pa_cache* c, const int32_t* slots, const int32_t
         a.inv_k = fp8 ? 1.0f / c->cfg.k_scale : 1.0f;
         a.inv_v = fp8 ? 1.0f / c->cfg.v_scale : 1.0f;
         pa::hip_check(pa::launch_append_batch(c->cfg.dtype, a, s), "append_batch kernel launch");
-        pa::hip_check(hipEventRecord(st.done, s), "hipEventRecord staging");
+        release_stage(st, s);
     });
 }
 
@@ -277,7 +247,7 @@ pa_status pa_cache_release(pa_cache* c, int slot) {
         if (!c) throw std::invalid_argument("cache is null");
         pool_release(c->pool, slot);
         // A batched append still in flight may write this slot's length.
-        for (pa_stage& st : c->stage)
+        for (pa_stage& st : c->append_staging.bufs)
             if (st.done) pa::hip_check(hipEventSynchronize(st.done), "hipEventSynchronize staging");
         pa::hip_check(hipMemset(c->d_seq_lens + slot, 0, sizeof(int32_t)), "hipMemset seq_len");
     });

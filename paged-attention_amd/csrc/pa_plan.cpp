@@ -113,20 +113,96 @@ void make_plan_impl(pa_plan& plan, int dtype, const int32_t* lens, int batch, in
     if (num_ctas <= 0) num_ctas = wave_ctas_impl(dtype, hd, group);
     cut(plan, tile, lens, batch, hkv, num_ctas);
 }
-void device_plan_upload(pa_device_plan& dp, const pa_plan& plan, int group, int head_dim, hipStream_t s) {
+pa_stage& take_stage(pa_stage_pool& sp, size_t need, bool with_device) {
+    const size_t n = sp.bufs.size();
+    size_t pick = n;
+    for (size_t k = 0; k < n && pick == n; ++k) {
+        const size_t i = (sp.next + k) % n;
+        const hipError_t q = hipEventQuery(sp.bufs[i].done);
+        if (q == hipSuccess) pick = i;
+        else if (q != hipErrorNotReady) pa::hip_check(q, "hipEventQuery staging");
+    }
+    if (pick == n) {
+        if (n < pa_stage_pool::kMaxStages) {
+            sp.bufs.emplace_back();
+            pa::hip_check(hipEventCreateWithFlags(&sp.bufs.back().done, hipEventDisableTiming), "hipEventCreate");
+        } else {
+            pick = sp.next % n;   // every buffer in flight: the oldest
+            pa::hip_check(hipEventSynchronize(sp.bufs[pick].done), "hipEventSynchronize staging");
+        }
+    }
+    sp.next = (pick + 1) % sp.bufs.size();
+    pa_stage& st = sp.bufs[pick];
+    if (st.cap < need || (with_device && !st.dev)) {
+        const size_t cap = std::max<size_t>(need + need / 2, 4096);
+        (void)hipHostFree(st.host);
+        (void)hipFree(st.dev);
+        st.host = nullptr;
+        st.dev  = nullptr;
+        st.cap  = 0;
+        pa::hip_check(hipHostMalloc(reinterpret_cast<void**>(&st.host), cap * sizeof(int32_t), hipHostMallocDefault),
+                      "hipHostMalloc staging");
+        if (with_device)
+            pa::hip_check(hipMalloc(reinterpret_cast<void**>(&st.dev), cap * sizeof(int32_t)), "hipMalloc staging");
+        st.cap = cap;
+    }
+    return st;
+}
+void release_stage(pa_stage& st, hipStream_t s) { pa::hip_check(hipEventRecord(st.done, s), "hipEventRecord staging"); }
+void free_stages(pa_stage_pool& sp) {
+    for (pa_stage& st : sp.bufs) {
+        if (st.done) (void)hipEventSynchronize(st.done);
+        (void)hipHostFree(st.host);
+        (void)hipFree(st.dev);
+        if (st.done) (void)hipEventDestroy(st.done);
+    }
+    sp = pa_stage_pool{};
+}
+void device_plan_upload(pa_device_plan& dp, const pa_plan& plan, int group, int head_dim, hipStream_t s,
+                        const int32_t* extra, size_t n_extra) {
     if (group <= 0 || head_dim <= 0) throw std::invalid_argument("upload: bad group or head_dim");
+    if (n_extra && !extra) throw std::invalid_argument("upload: extra ints are null");
     const size_t nseg = plan.segments.size() / 4;
     // The kernels read a 16-token group from one page run (page sizes >= 16) or
     // one 1 KiB part from one page: a segment may only start on a group boundary.
     for (size_t i = 0; i < nseg; ++i)
         if (plan.segments[4 * i + 2] % pa::kGroupTokens != 0)
             throw std::invalid_argument("upload: segment starts must be multiples of 16 tokens");
-    upload_grow(dp.segments, dp.seg_cap, plan.segments.data(), plan.segments.size(), s);
-    upload_grow(dp.cta_seg_begin, dp.cta_cap, plan.cta_seg_begin.data(), plan.cta_seg_begin.size(), s);
-    upload_grow(dp.item_seg_begin, dp.item_cap, plan.item_seg_begin.data(), plan.item_seg_begin.size(), s);
+    // One block: segments | cta_seg_begin | item_seg_begin | extra, each part
+    // starting on a 16-byte boundary (the kernels read segments as int4).
+    auto round4 = [](size_t n) { return (n + 3) & ~size_t{3}; };
+    const size_t o_cta   = round4(plan.segments.size());
+    const size_t o_item  = o_cta + round4(plan.cta_seg_begin.size());
+    const size_t o_extra = o_item + round4(plan.item_seg_begin.size());
+    const size_t total   = o_extra + round4(n_extra);
+    if (total > dp.ints_cap) {
+        // Growing frees the old block, which decodes queued before may still
+        // read: wait for them first (growth only happens for a plan larger
+        // than every earlier one).
+        pa::hip_check(hipStreamSynchronize(s), "hipStreamSynchronize");
+        pa::hip_check(hipFree(dp.ints), "hipFree");
+        dp.ints = nullptr;
+        dp.ints_cap = 0;
+        const size_t cap = std::max<size_t>(total + total / 4, 1024);
+        pa::hip_check(hipMalloc(reinterpret_cast<void**>(&dp.ints), cap * sizeof(int32_t)), "hipMalloc plan");
+        dp.ints_cap = cap;
+    }
+    pa_stage& st = take_stage(dp.staging, total, false);
+    std::copy(plan.segments.begin(), plan.segments.end(), st.host);
+    std::copy(plan.cta_seg_begin.begin(), plan.cta_seg_begin.end(), st.host + o_cta);
+    std::copy(plan.item_seg_begin.begin(), plan.item_seg_begin.end(), st.host + o_item);
+    if (n_extra) std::copy(extra, extra + n_extra, st.host + o_extra);
+    pa::hip_check(hipMemcpyAsync(dp.ints, st.host, total * sizeof(int32_t), hipMemcpyHostToDevice, s),
+                  "hipMemcpyAsync plan");
+    release_stage(st, s);
+    dp.segments       = dp.ints;
+    dp.cta_seg_begin  = dp.ints + o_cta;
+    dp.item_seg_begin = dp.ints + o_item;
+    dp.extra          = n_extra ? dp.ints + o_extra : nullptr;
     const size_t rows = nseg * static_cast<size_t>(group);
     const size_t need = rows * (static_cast<size_t>(head_dim) + 1);
     if (need > dp.part_cap) {
+        pa::hip_check(hipStreamSynchronize(s), "hipStreamSynchronize");   // queued decodes may still use it
         pa::hip_check(hipFree(dp.partial_out), "hipFree");
         dp.partial_out = nullptr;
         pa::hip_check(hipMalloc(reinterpret_cast<void**>(&dp.partial_out), sizeof(float) * need), "hipMalloc");
@@ -161,8 +237,6 @@ void device_plan_upload(pa_device_plan& dp, const pa_plan& plan, int group, int 
     dp.max_item_segments = 0;
     for (int i = 0; i < plan.items; ++i)
         dp.max_item_segments = std::max(dp.max_item_segments, plan.item_seg_begin[i + 1] - plan.item_seg_begin[i]);
-    // The sources are host vectors the caller may free or rebuild right away.
-    pa::hip_check(hipStreamSynchronize(s), "hipStreamSynchronize");
 }
 void device_plan_bind(const pa_device_plan& dp, pa_decode_params& p) {
     p.segments       = dp.segments;
@@ -176,9 +250,8 @@ void device_plan_bind(const pa_device_plan& dp, pa_decode_params& p) {
     p.block_merge       = dp.block_merge ? 1 : 0;
 }
 void device_plan_free(pa_device_plan& dp) {
-    (void)hipFree(dp.segments);
-    (void)hipFree(dp.cta_seg_begin);
-    (void)hipFree(dp.item_seg_begin);
+    free_stages(dp.staging);
+    (void)hipFree(dp.ints);
     (void)hipFree(dp.partial_out);
     dp = pa_device_plan{};
 }

@@ -1,7 +1,8 @@
 """GPU tests of the cache side of the path, through the C ABI: the FP8
 append-quantizer and page scatter (bit-exact against the oracle), the
 block-table resolution probe, batched appends (paged_kv_cache.cu:95-136 grown
-to a decode step's batch) and PagedKVCache::plan over a subset of slots.
+to a decode step's batch), PagedKVCache::plan over a subset of slots, and
+planning the next step while the previous one is still queued.
 """
 
 from __future__ import annotations
@@ -196,3 +197,88 @@ def test_cache_plan_subset_of_slots_in_any_order(fp8):
     got = out.float().cpu().numpy()
     assert float(np.max(np.abs(got - ref))) < TOL
     cache.close()
+
+
+def _busy_stream(ms_of_reads: int = 20):
+    """Queues ~ms_of_reads x 0.16 ms of plain 1 GiB reads on the current stream
+    and returns an event recorded after them (the reads keep the stream busy)."""
+    import torch
+    buf = torch.ones(1 << 30, dtype=torch.uint8, device="cuda")
+    sink = torch.zeros(1, dtype=torch.int32, device="cuda")
+    for _ in range(ms_of_reads):
+        pa_amd.stream_read_chunked(buf, buf.numel(), 256, sink)
+    ev = torch.cuda.Event()
+    ev.record()
+    return ev, buf
+
+
+@pytest.mark.parametrize("fp8", DTYPES, ids=IDS)
+def test_plan_next_step_while_previous_is_queued(fp8):
+    """PagedKVCache::plan (decode.cu:131-146 DevicePlan::upload under it) queues
+    its copies from pinned staging and does not synchronize the stream: with
+    ~3 ms of reads queued, plan() returns while they still run; a sequence of
+    steps (different slot subsets and orders, a re-plan of an earlier one)
+    planned and run back to back without any synchronization equals,
+    bitwise, the same steps each planned, run and synchronized alone."""
+    import torch
+    hq, hkv = 32, 8
+    lens = [3000, 17, 1, 4100, 700, 16384]
+    pages = [math.ceil(L / 16) for L in lens]
+    dt = pa_amd.FP8_E4M3 if fp8 else pa_amd.FP16
+    cache = pa_amd.PagedKVCache(sum(pages) + 8, 16, hkv, D, len(lens), max(pages), dt, 0.02, 0.02)
+    cache.shuffle_free_pages(5)
+    g = torch.Generator(device="cuda").manual_seed(2)
+    for L in lens:
+        s_ = cache.admit()
+        k = torch.randn(L, hkv, D, device="cuda", dtype=torch.float16, generator=g)
+        assert cache.append(s_, k, torch.randn_like(k), L)
+    steps = [[0, 1, 2, 3, 4, 5], [5, 3, 1], [2], [4, 0], [0, 1, 2, 3, 4, 5], [1, 5]]
+    qs = [torch.randn(len(s_), hq, D, device="cuda", dtype=torch.float16, generator=g) for s_ in steps]
+    ref = []
+    for slots, q in zip(steps, qs):
+        out = torch.empty_like(q)
+        cache.plan(slots, hq)
+        cache.run(q, out)
+        torch.cuda.synchronize()
+        ref.append(out)
+    ev, buf = _busy_stream()
+    outs = []
+    for i, (slots, q) in enumerate(zip(steps, qs)):
+        cache.plan(slots, hq)
+        if i == 0:
+            assert not ev.query(), "plan() waited for work queued before it"
+        outs.append(torch.empty_like(q))
+        cache.run(q, outs[-1])
+    assert not ev.query(), "the queued steps synchronized the stream"
+    torch.cuda.synchronize()
+    for i, (a, b) in enumerate(zip(outs, ref)):
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16)), f"step {i} differs"
+    cache.close()
+
+
+def test_decoder_plan_while_previous_run_is_queued():
+    """The torch Decoder: run() with plan A, then plan(B) and run() without a
+    synchronization in between (and with the stream busy): each output equals
+    the eager one; plan(B) returns before the queued work is done."""
+    import torch
+    from helpers import paged_inputs
+    lens_a, lens_b = [1024] * 4, [300, 5000, 77, 1]
+    qa, ka, va, ta, _, _ = paged_inputs(4, lens_a, 32, 8, 16, False, seed=3)
+    qb, kb, vb, tb, _, _ = paged_inputs(4, lens_b, 32, 8, 16, False, seed=4)
+    la, lb = torch.tensor(lens_a, dtype=torch.int32), torch.tensor(lens_b, dtype=torch.int32)
+    la_dev, lb_dev = la.cuda(), lb.cuda()        # (a blocking copy would synchronize the stream)
+    dec = pa_amd.Decoder(32, 8, D, 16, False)
+    dec.plan(la)
+    ref_a = dec.run(qa, ka, va, ta, la_dev, 1.0, 1.0)
+    dec.plan(lb)
+    ref_b = dec.run(qb, kb, vb, tb, lb_dev, 1.0, 1.0)
+    torch.cuda.synchronize()
+    ev, buf = _busy_stream()
+    dec.plan(la)
+    out_a = dec.run(qa, ka, va, ta, la_dev, 1.0, 1.0)
+    dec.plan(lb)
+    assert not ev.query(), "Decoder.plan waited for queued work"
+    out_b = dec.run(qb, kb, vb, tb, lb_dev, 1.0, 1.0)
+    torch.cuda.synchronize()
+    assert torch.equal(out_a.view(torch.int16), ref_a.view(torch.int16))
+    assert torch.equal(out_b.view(torch.int16), ref_b.view(torch.int16))
