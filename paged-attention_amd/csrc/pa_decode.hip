@@ -110,6 +110,13 @@
 #ifndef PA_FP16_LDS_STAGE
 #define PA_FP16_LDS_STAGE 0
 #endif
+// 1: every LDS-staged path fills the stage with LDS-destination loads
+// (buffer / global_load_dwordx4 ... lds: 16 bytes per lane land at M0 + 16 *
+// lane, no VGPRs, no ds_write), one step in flight; 0: loads into VGPRs, then
+// ds_write, with the path's tuned depth.
+#ifndef PA_LDS_DMA
+#define PA_LDS_DMA 1
+#endif
 
 namespace pa {
 namespace {
@@ -131,6 +138,25 @@ template <int EB> struct Tune {
 };
 static_assert(Tune<2>::step == 16 || Tune<2>::step == 32, "fp16 step must be 16 or 32");
 static_assert(Tune<1>::step == 16 || Tune<1>::step == 32, "fp8 step must be 16 or 32");
+constexpr bool kLdsDma = PA_LDS_DMA != 0;
+
+// LDS-destination load of 16 bytes per lane: lane i's bytes land at dst + 16 i
+// (AUX: the cache-policy operand, 2 = non-temporal).
+template <int AUX>
+__device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t rs, u32x4* dst, int voffset) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)dst, 16, voffset, 0, 0,
+                                             AUX);
+}
+template <int AUX>
+__device__ __forceinline__ void lds_load16(const void* src, u32x4* dst) {
+    __builtin_amdgcn_global_load_lds((__attribute__((address_space(1))) void*)const_cast<void*>(src),
+                                     (__attribute__((address_space(3))) void*)dst, 16, 0, AUX);
+}
+// s_waitcnt immediates (gfx9 encoding: vmcnt [3:0] and [15:14], expcnt [6:4],
+// lgkmcnt [11:8]): wait for every vector memory operation (LDS-destination
+// loads included), or for every LDS / scalar memory operation.
+constexpr int kWaitVm0   = 0x0F70;
+constexpr int kWaitLgkm0 = 0xC07F;
 
 // How a step finds its pages.
 enum PagePath : int {
@@ -289,6 +315,8 @@ __device__ __forceinline__ void decode_split_body(const pa_decode_params& p, int
     constexpr int  NPART = 16 / RPP;                // parts per 16-token half
     constexpr int  CPR   = ROW / 16;                // 16-byte chunks per row
     constexpr int  HCH   = 16 * CPR;                // 16-byte chunks per half (256 B per row x 16)
+    constexpr bool DMA   = STG && kLdsDma;          // the stage is filled by LDS-destination loads
+    static_assert(!DMA || DEPTH == 1, "the LDS-destination stage holds one step");
     using VRaw = std::conditional_t<EB == 2, u32x4, u32x2>;
     using KRaw = std::conditional_t<KL == 16, u32x4, u32x2>;
 
@@ -329,13 +357,22 @@ __device__ __forceinline__ void decode_split_body(const pa_decode_params& p, int
     // Constant lane offsets inside a 16-token half (power-of-two path).
     const int k_lane_off = c * ROW + kb * KLANE;
     const int v_lane_off = 4 * kb * ROW + c * VCH;
+    // LDS-destination stage: lane i of 1 KiB part `part` lands in slot 64 part +
+    // i, i.e. row RPP part + i / CPR, chunk position i % CPR, which holds
+    // chunk (i % CPR) ^ (row % CPR) of that row (the swizzle moves to the
+    // source): dma_chunk[part] is that chunk's byte offset within its row.
+    int dma_chunk[NPART];
+#pragma unroll
+    for (int part = 0; part < NPART; ++part)
+        dma_chunk[part] = 16 * ((lane % CPR) ^ ((RPP * part + lane / CPR) % CPR));
+    u32x4* const stage = stage_lds[STG ? wave : 0];
 
     // ---- pipeline registers, indexed by ring slot = step index mod DEPTH
     KRaw  kr[DEPTH][NH][NK];   // K: token 16hh + c of each half
     VRaw  vr[DEPTH][NH][4];    // V: tokens 16hh + 4kb + r, dims 8c..8c+7
     // LDS-staged FP8: the raw coalesced loads (rows 8 part + lane / 8, bytes
     // 16 (lane % 8) .. +15 of each half), moved into kr / vr by the stage.
-    u32x4 kc[STG ? DEPTH : 1][NH][NPART], vc[STG ? DEPTH : 1][NH][NPART];
+    u32x4 kc[STG && !DMA ? DEPTH : 1][NH][NPART], vc[STG && !DMA ? DEPTH : 1][NH][NPART];
     u32x4 qc[DEPTH][NQ];       // compact Q, loaded with a segment's first step
     int   pg[DEPTH][NH];       // power-of-two path: page of each half (wave-uniform)
     int   pgr[PATH == kPageRuns ? DEPTH : 1][NH][NPART];   // small pages: page of each part
@@ -427,6 +464,11 @@ __device__ __forceinline__ void decode_split_body(const pa_decode_params& p, int
 
     // K/V loads of step L into slot s (and Q at a segment start), then advance L.
     auto issue = [&](int s) {
+        if constexpr (DMA) {
+            // The previous step's stage reads have returned before new rows land.
+            __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+            wave_lds_sync();
+        }
         const bool first = l_more && L.tok == L.t0;
         const __amdgpu_buffer_rsrc_t qrs =
             buffer_rsrc(p.q + (static_cast<size_t>(L.b) * hq + L.h * G) * kHeadDim, first ? 256 * G : 0);
@@ -447,7 +489,15 @@ __device__ __forceinline__ void decode_split_body(const pa_decode_params& p, int
                                     static_cast<uint32_t>((L.h * P + (bt & (P - 1))) * ROW);
                 const __amdgpu_buffer_rsrc_t krs = buffer_rsrc(kbase + row0, nv * ROW);
                 const __amdgpu_buffer_rsrc_t vrs = buffer_rsrc(vbase + row0, nv * ROW);
-                if constexpr (STG) {
+                if constexpr (DMA) {
+#pragma unroll
+                    for (int part = 0; part < NPART; ++part) {
+                        const int off = 1024 * part + ROW * (lane / CPR) + dma_chunk[part];
+                        lds_load16<kAux<NT>>(krs, stage + hh * HCH + 64 * part, off);
+                        lds_load16<kAux<NT>>(vrs, stage + (NH + hh) * HCH + 64 * part, off);
+                    }
+                    continue;
+                } else if constexpr (STG) {
 #pragma unroll
                     for (int part = 0; part < NPART; ++part) {
                         kc[s][hh][part] = __builtin_bit_cast(
@@ -489,10 +539,16 @@ __device__ __forceinline__ void decode_split_body(const pa_decode_params& p, int
                         static_cast<uint32_t>((L.h * P + (bt & (P - 1))) * ROW);
                     const __amdgpu_buffer_rsrc_t krs = buffer_rsrc(kbase + row0, nv * ROW);
                     const __amdgpu_buffer_rsrc_t vrs = buffer_rsrc(vbase + row0, nv * ROW);
-                    kc[s][hh][part] = __builtin_bit_cast(
-                        u32x4, __builtin_amdgcn_raw_buffer_load_b128(krs, 16 * lane, 0, kAux<NT>));
-                    vc[s][hh][part] = __builtin_bit_cast(
-                        u32x4, __builtin_amdgcn_raw_buffer_load_b128(vrs, 16 * lane, 0, kAux<NT>));
+                    if constexpr (DMA) {
+                        const int off = ROW * (lane / CPR) + dma_chunk[part];
+                        lds_load16<kAux<NT>>(krs, stage + hh * HCH + 64 * part, off);
+                        lds_load16<kAux<NT>>(vrs, stage + (NH + hh) * HCH + 64 * part, off);
+                    } else {
+                        kc[s][hh][part] = __builtin_bit_cast(
+                            u32x4, __builtin_amdgcn_raw_buffer_load_b128(krs, 16 * lane, 0, kAux<NT>));
+                        vc[s][hh][part] = __builtin_bit_cast(
+                            u32x4, __builtin_amdgcn_raw_buffer_load_b128(vrs, 16 * lane, 0, kAux<NT>));
+                    }
                 }
         } else if constexpr (PATH == kPageLane) {
 #pragma unroll
@@ -500,9 +556,14 @@ __device__ __forceinline__ void decode_split_body(const pa_decode_params& p, int
 #pragma unroll
                 for (int part = 0; part < NPART; ++part) {
                     const int pgl = __builtin_amdgcn_ds_bpermute(plk[s][hh][part], pent[s]);
-                    const size_t off = kv_row_offset<EB>(pgl, L.h, psl[s][hh][part], P, hkv) + 16 * (lane % CPR);
-                    kc[s][hh][part] = load16<NT>(kbase + off);
-                    vc[s][hh][part] = load16<NT>(vbase + off);
+                    const size_t row = kv_row_offset<EB>(pgl, L.h, psl[s][hh][part], P, hkv);
+                    if constexpr (DMA) {
+                        lds_load16<kAux<NT>>(kbase + row + dma_chunk[part], stage + hh * HCH + 64 * part);
+                        lds_load16<kAux<NT>>(vbase + row + dma_chunk[part], stage + (NH + hh) * HCH + 64 * part);
+                    } else {
+                        kc[s][hh][part] = load16<NT>(kbase + row + 16 * (lane % CPR));
+                        vc[s][hh][part] = load16<NT>(vbase + row + 16 * (lane % CPR));
+                    }
                 }
         } else {
 #pragma unroll
@@ -629,19 +690,27 @@ __device__ __forceinline__ void decode_split_body(const pa_decode_params& p, int
         if constexpr (STG) {
             // Coalesced rows -> LDS (16-byte chunk j of row r at chunk j ^ (r % CPR))
             // -> the K / V lane layouts of the direct loads.
-            u32x4* st = stage_lds[wave];
-            const int wrow = lane / CPR;   // row within a 1 KiB part
-            wave_lds_sync();   // the previous step's stage reads are done
+            u32x4* st = stage;
+            if constexpr (DMA) {
+                // With one step in flight, every vector memory operation
+                // outstanding here belongs to this step: its rows are in the
+                // stage once they have all returned.
+                __builtin_amdgcn_s_waitcnt(kWaitVm0);
+                wave_lds_sync();
+            } else {
+                const int wrow = lane / CPR;   // row within a 1 KiB part
+                wave_lds_sync();   // the previous step's stage reads are done
 #pragma unroll
-            for (int hh = 0; hh < NH; ++hh)
+                for (int hh = 0; hh < NH; ++hh)
 #pragma unroll
-                for (int part = 0; part < NPART; ++part) {
-                    const int row  = RPP * part + wrow;
-                    const int slot = CPR * row + ((lane % CPR) ^ (row % CPR));
-                    st[hh * HCH + slot]        = kc[s][hh][part];
-                    st[(NH + hh) * HCH + slot] = vc[s][hh][part];
-                }
-            wave_lds_sync();   // every lane's rows land before any lane reads its layout
+                    for (int part = 0; part < NPART; ++part) {
+                        const int row  = RPP * part + wrow;
+                        const int slot = CPR * row + ((lane % CPR) ^ (row % CPR));
+                        st[hh * HCH + slot]        = kc[s][hh][part];
+                        st[(NH + hh) * HCH + slot] = vc[s][hh][part];
+                    }
+                wave_lds_sync();   // every lane's rows land before any lane reads its layout
+            }
 #pragma unroll
             for (int hh = 0; hh < NH; ++hh) {
 #pragma unroll
@@ -933,7 +1002,11 @@ __global__ __launch_bounds__(64 * WAVES) void decode_merge_kernel(const pa_decod
 #ifndef PA_FP8_LANE_DEPTH
 #define PA_FP8_LANE_DEPTH 2
 #endif
-template <int EB> constexpr int kLaneDepth = EB == 2 ? PA_FP16_LANE_DEPTH : PA_FP8_LANE_DEPTH;
+template <int EB> constexpr int kLaneDepth = kLdsDma ? 1 : EB == 2 ? PA_FP16_LANE_DEPTH : PA_FP8_LANE_DEPTH;
+// Steps in flight on the power-of-two path (one when it is staged through
+// LDS-destination loads) and on the staged small-page path.
+template <int EB> constexpr int kPow2Depth = kLdsDma && Tune<EB>::stage ? 1 : Tune<EB>::depth;
+template <int EB> constexpr int kRunsDepth = kLdsDma ? 1 : Tune<EB>::depth;
 
 template <int EB, int G, int NG, int DEPTH, int PATH>
 hipError_t launch_split_p(const pa_decode_params& p, int shift, hipStream_t s) {
@@ -956,14 +1029,14 @@ hipError_t launch_split_g(const pa_decode_params& p, hipStream_t s) {
         // Byte offsets of one page and of one (kv head, slot) inside it are 32-bit.
         if (static_cast<long long>(p.num_kv_heads) * P * kRowBytes<EB> >= (1ll << 31))
             throw std::invalid_argument("decode: page_size * num_kv_heads * row bytes must be below 2^31");
-        return launch_split_p<EB, G, Tune<EB>::step, Tune<EB>::depth, kPagePow2>(p, shift, s);
+        return launch_split_p<EB, G, Tune<EB>::step, kPow2Depth<EB>, kPagePow2>(p, shift, s);
     }
     if constexpr (EB == 2 || Tune<EB>::stage) {
         // Pages of whole 1 KiB parts (4 fp16 rows, 8 FP8 rows) through the LDS stage.
         if (P == 8 || (EB == 2 && P == 4)) {
             if (static_cast<long long>(p.num_kv_heads) * P * kRowBytes<EB> >= (1ll << 31))
                 throw std::invalid_argument("decode: page_size * num_kv_heads * row bytes must be below 2^31");
-            return launch_split_p<EB, G, Tune<EB>::step, Tune<EB>::depth, kPageRuns>(p, shift, s);
+            return launch_split_p<EB, G, Tune<EB>::step, kRunsDepth<EB>, kPageRuns>(p, shift, s);
         }
         // Any other size: per-lane rows through the LDS stage (shift -1: divide).
         return launch_split_p<EB, G, Tune<EB>::step, kLaneDepth<EB>, kPageLane>(p, pow2 ? shift : -1, s);
@@ -1024,10 +1097,10 @@ template <int EB, int G>
 const void* split_symbol() {
     if constexpr (EB == 2)
         return reinterpret_cast<const void*>(
-            &decode_split_kernel_f16<G, Tune<EB>::step, Tune<EB>::depth, kPagePow2>);
+            &decode_split_kernel_f16<G, Tune<EB>::step, kPow2Depth<EB>, kPagePow2>);
     else
         return reinterpret_cast<const void*>(
-            &decode_split_kernel_fp8<G, Tune<EB>::step, Tune<EB>::depth, kPagePow2>);
+            &decode_split_kernel_fp8<G, Tune<EB>::step, kPow2Depth<EB>, kPagePow2>);
 }
 
 }  // namespace
