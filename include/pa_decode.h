@@ -209,6 +209,13 @@ pa_status pa_stream_read_chunked(const void* buf, size_t bytes, int blocks, int 
  * bench inputs; here it is a write of known size for counter calibration). */
 pa_status pa_fill_bytes(void* buf, size_t bytes, int value, void* stream);
 
+/* n device elements fp32 -> fp16 (round to nearest even) and fp16 -> fp32
+ * (exact). No counterpart of their own in the reference: the legacy pool's FP32
+ * device entry (src/attention/paged_pool/pool.hpp:21-24 decode_device) converts
+ * its q and out with them around the fp16 decode. */
+pa_status pa_f32_to_f16(const float* in, uint16_t* out, size_t n, void* stream);
+pa_status pa_f16_to_f32(const uint16_t* in, float* out, size_t n, void* stream);
+
 /* ---- host page pool (paged_kv_cache.cu:84-151, no device memory) -------- */
 
 typedef struct pa_pool pa_pool;

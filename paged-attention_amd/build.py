@@ -95,5 +95,43 @@ def build_bench(verbose: bool = False) -> pathlib.Path:
     return BENCH_BIN
 
 
+TORCH_EXT_SRC = CSRC / "pa_torch.cpp"
+TORCH_EXT_NAME = "_pa_torch"
+
+
+def torch_ext_path() -> pathlib.Path:
+    """Where the compiled torch binding goes: inside the pa_amd package."""
+    import sysconfig
+    return PKG / "pa_amd" / (TORCH_EXT_NAME + sysconfig.get_config_var("EXT_SUFFIX"))
+
+
+def build_torch_ext(verbose: bool = False) -> pathlib.Path:
+    """The compiled torch binding (csrc/pa_torch.cpp: Decoder, the reference's
+    bindings/torch_decode.cu signature) against lib/libpa_decode.so and the
+    installed torch (host code only; its headers need the HIP platform macro)."""
+    import sysconfig
+
+    import torch
+    from torch.utils import cpp_extension as ce
+
+    out = torch_ext_path()
+    incs = ce.include_paths(device_type="cuda") + [sysconfig.get_paths()["include"], str(ROOT / "include")]
+    libs = ce.library_paths(device_type="cuda")
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    tmp = out.with_suffix(".so.tmp")
+    cmd = [os.environ.get("CXX", "g++"), "-O2", "-std=c++17", "-fPIC", "-shared", "-w",
+           f"-DTORCH_EXTENSION_NAME={TORCH_EXT_NAME}", "-DTORCH_API_INCLUDE_EXTENSION_H",
+           "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+           *[f"-I{p}" for p in incs], str(TORCH_EXT_SRC), "-o", str(tmp),
+           *[f"-L{p}" for p in libs], f"-L{LIB_DIR}",
+           "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu", "-ltorch_hip", "-ltorch_python", "-lpa_decode",
+           f"-Wl,-rpath,$ORIGIN/../lib", f"-Wl,-rpath,{libs[0]}"]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    _run(cmd)
+    os.replace(tmp, out)
+    return out
+
+
 if __name__ == "__main__":
     print(build(verbose="-v" in sys.argv))

@@ -19,7 +19,14 @@
 //     std::length_error when append_token finds no free page or a sequence
 //     would exceed max_pages_per_seq. admit() returns -1 when no slot or not
 //     enough pages are free, as in the reference.
-//   * The FP32 device-pointer entry decode_device() is not provided.
+//   * decode_device() takes fp32 device q / out as the reference's does; q is
+//     rounded to fp16 on the device and the fp16 output widened back. The
+//     three partial buffers are accepted and unused (the plan's own workspace
+//     holds the split partials). Like the reference it launches on the default
+//     stream and does not synchronize.
+//   * kv_K_base() / kv_V_base() return the fp16 (or E4M3) pools as const void*.
+//   * paged_max_sequences_for_budget() counts this pool's element size (fp16 by
+//     default, one byte for FP8) where the reference's counts fp32.
 
 #include "attention_backend.hpp"
 #include "decode/half_host.hpp"
@@ -44,11 +51,18 @@ public:
           d_(d) {
         HIP_CHECK(hipMalloc(&d_q_, sizeof(uint16_t) * static_cast<size_t>(d)));
         HIP_CHECK(hipMalloc(&d_out_, sizeof(uint16_t) * static_cast<size_t>(d)));
+        // Slot ids 0 .. max_sequences - 1: decode_device points a plan's slot
+        // indirection at entry `slot` instead of copying the id per call.
+        std::vector<int32_t> ids(static_cast<size_t>(max_sequences));
+        for (int i = 0; i < max_sequences; ++i) ids[static_cast<size_t>(i)] = i;
+        HIP_CHECK(hipMalloc(&d_slots_, sizeof(int32_t) * ids.size()));
+        HIP_CHECK(hipMemcpy(d_slots_, ids.data(), sizeof(int32_t) * ids.size(), hipMemcpyHostToDevice));
     }
     ~PagedPool() override {
         (void)hipFree(d_q_);
         (void)hipFree(d_out_);
         (void)hipFree(d_kv_);
+        (void)hipFree(d_slots_);
     }
     PagedPool(const PagedPool&)            = delete;
     PagedPool& operator=(const PagedPool&) = delete;
@@ -98,6 +112,33 @@ public:
         for (int i = 0; i < d_; ++i) h_out[i] = decode::f16_to_f32(h[static_cast<size_t>(i)]);
     }
 
+    // pool.hpp:21-24 decode_device: out[d] (fp32, device) = attention of q[d]
+    // (fp32, device) over the first actual_len rows of the slot. Launches on the
+    // default stream and returns without synchronizing. The partial buffers of
+    // the reference's signature are not used.
+    void decode_device(int slot, int actual_len, const float* d_q, float* d_out, float* d_partial_out = nullptr,
+                       float* d_partial_max = nullptr, float* d_partial_sum = nullptr) const {
+        (void)d_partial_out;
+        (void)d_partial_max;
+        (void)d_partial_sum;
+        if (!is_occupied(slot)) throw std::invalid_argument("PagedPool::decode_device: slot is not admitted");
+        if (actual_len <= 0 || actual_len > cache_.seq_len(slot))
+            throw std::invalid_argument("PagedPool::decode_device: actual_len must be in 1 .. the slot's length");
+        if (!d_q || !d_out) throw std::invalid_argument("PagedPool::decode_device: null q or out");
+        const decode::KVDtype dt = cache_.config().dtype;
+        dplan_.upload(decode::make_plan(dt, {actual_len}, 1, 1, d_), 1, d_, 0);
+        decode::detail::check(pa_f32_to_f16(d_q, d_q_, static_cast<size_t>(d_), nullptr));
+        decode::DecodeParams p = cache_.params();
+        p.q           = half_ptr(d_q_);
+        p.out         = reinterpret_cast<half*>(d_out_);
+        p.slot_ids    = d_slots_ + slot;
+        p.batch       = 1;
+        p.num_q_heads = 1;
+        dplan_.bind(p);
+        decode::paged_decode(dt, p, 0);
+        decode::detail::check(pa_f16_to_f32(d_out_, d_out, static_cast<size_t>(d_), nullptr));
+    }
+
     int  actual_len(int slot) const override { return is_occupied(slot) ? cache_.seq_len(slot) : 0; }
     bool is_occupied(int slot) const override {
         return slot >= 0 && slot < cache_.config().max_slots && cache_.occupied(slot);
@@ -107,6 +148,10 @@ public:
     int    max_sequences() const { return cache_.config().max_slots; }
     int    d() const { return d_; }
     size_t total_kv_bytes() const { return cache_.total_bytes(); }
+    // pool.hpp:34-35: the device K and V pools ([pages][1][page_size][d], fp16
+    // or E4M3 bytes).
+    const void* kv_K_base() const { return cache_.params().k_cache; }
+    const void* kv_V_base() const { return cache_.params().v_cache; }
     // The cache underneath (block tables, params() for the batched kernels).
     decode::PagedKVCache&       cache() { return cache_; }
     const decode::PagedKVCache& cache() const { return cache_; }
@@ -155,7 +200,29 @@ private:
     uint16_t*             d_kv_  = nullptr;
     size_t                cap_   = 0;
     std::vector<uint16_t> host_;
+    int32_t*              d_slots_ = nullptr;   // [max_sequences]: i at entry i
+    // decode_device's plan (the method is const in the reference's interface).
+    mutable decode::DevicePlan dplan_;
 };
+
+// pool.hpp:63-67: sequences of actual_len tokens that fit budget_bytes of
+// this pool's pages (K and V, page_size x d elements each, 2 bytes per fp16
+// element or 1 per E4M3 one).
+inline int paged_max_sequences_for_budget(size_t budget_bytes, int actual_len, int d, int page_size = PAGE_SIZE,
+                                          decode::KVDtype dtype = decode::KVDtype::FP16) {
+    if (actual_len <= 0 || d <= 0 || page_size <= 0)
+        throw std::invalid_argument("paged_max_sequences_for_budget: sizes must be positive");
+    const int    pages_per_seq = (actual_len + page_size - 1) / page_size;
+    const size_t per_page      = 2ull * static_cast<size_t>(decode::kv_dtype_bytes(dtype)) *
+                                 static_cast<size_t>(page_size) * static_cast<size_t>(d);
+    return static_cast<int>(budget_bytes / per_page) / pages_per_seq;
+}
+
+// pool.hpp:69-72: slots left empty in the last page of a sequence.
+inline int paged_waste_tokens(int actual_len, int page_size = PAGE_SIZE) {
+    const int pages = (actual_len + page_size - 1) / page_size;
+    return pages * page_size - actual_len;
+}
 
 // One query over T rows through a single-use PagedPool sized to fit them
 // (src/attention/paged_pool/pool.cu:159-166).

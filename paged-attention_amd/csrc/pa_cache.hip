@@ -8,6 +8,7 @@
 //   stream_read_chunked_kernel  the same read with one contiguous span per wave (best read rate)
 //   fill_bytes_kernel    streaming write of a byte value (bench_decode.cu:61-68's fill role; the
 //                        write-side counterpart of the copy ceiling)
+//   f32_to_f16_kernel, f16_to_f32_kernel  element conversions for the legacy pool's fp32 device entry
 
 #include "pa_device.hpp"
 
@@ -258,6 +259,20 @@ __global__ __launch_bounds__(512) void stream_read_chunked_kernel(const unsigned
     if (publish) *sink = acc;   // as in stream_read_kernel: never taken, keeps the loads
 }
 
+// fp32 -> fp16 (round to nearest even) and fp16 -> fp32 (exact), n elements.
+__global__ __launch_bounds__(256) void f32_to_f16_kernel(const float* __restrict__ in, uint16_t* __restrict__ out,
+                                                         size_t n) {
+    const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+    for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride)
+        out[i] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(in[i]));
+}
+__global__ __launch_bounds__(256) void f16_to_f32_kernel(const uint16_t* __restrict__ in, float* __restrict__ out,
+                                                         size_t n) {
+    const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+    for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride)
+        out[i] = static_cast<float>(__builtin_bit_cast(_Float16, in[i]));
+}
+
 // Streaming write: every 16-byte word of x gets `word` repeated.
 __global__ __launch_bounds__(256) void fill_bytes_kernel(u32x4* __restrict__ x, size_t n, uint32_t word) {
     const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
@@ -306,6 +321,19 @@ hipError_t launch_gather(int dtype, const void* cache, const int32_t* bt_row, in
     else
         hipLaunchKernelGGL(gather_kernel<1>, dim3(blocks), dim3(256), 0, s, cache, bt_row, hkv, page_size, kv_head,
                            len, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_convert(const void* in, void* out, size_t n, bool to_half, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    const size_t want = (n + 255) / 256;
+    const int blocks = static_cast<int>(want < 4096 ? want : 4096);
+    if (to_half)
+        hipLaunchKernelGGL(f32_to_f16_kernel, dim3(blocks), dim3(256), 0, s, static_cast<const float*>(in),
+                           static_cast<uint16_t*>(out), n);
+    else
+        hipLaunchKernelGGL(f16_to_f32_kernel, dim3(blocks), dim3(256), 0, s, static_cast<const uint16_t*>(in),
+                           static_cast<float*>(out), n);
     return hipGetLastError();
 }
 

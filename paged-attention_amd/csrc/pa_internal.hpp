@@ -83,6 +83,8 @@ hipError_t launch_append_batch(int dtype, const AppendBatch& a, hipStream_t s);
 hipError_t launch_gather(int dtype, const void* cache, const int32_t* bt_row, int hkv,
                          int page_size, int kv_head, int len, void* out, hipStream_t s);
 hipError_t launch_fill_bytes(void* buf, size_t bytes, int value, hipStream_t s);
+// n elements fp32 -> fp16 (RNE) when to_half, else fp16 -> fp32.
+hipError_t launch_convert(const void* in, void* out, size_t n, bool to_half, hipStream_t s);
 hipError_t launch_stream_read_chunked(const void* buf, size_t bytes, int blocks, int threads, int unroll,
                                      uint32_t* sink, hipStream_t s);
 hipError_t launch_stream_read(const void* buf, size_t bytes, int blocks, int threads, int unroll, bool nt,

@@ -486,6 +486,20 @@ pa_status pa_stream_read_ex(const void* buf, size_t bytes, int blocks, int threa
     });
 }
 
+pa_status pa_f32_to_f16(const float* in, uint16_t* out, size_t n, void* stream) {
+    return guarded([&] {
+        if (n && (!in || !out)) throw std::invalid_argument("f32_to_f16: null pointer");
+        pa::hip_check(pa::launch_convert(in, out, n, true, as_stream(stream)), "convert kernel launch");
+    });
+}
+
+pa_status pa_f16_to_f32(const uint16_t* in, float* out, size_t n, void* stream) {
+    return guarded([&] {
+        if (n && (!in || !out)) throw std::invalid_argument("f16_to_f32: null pointer");
+        pa::hip_check(pa::launch_convert(in, out, n, false, as_stream(stream)), "convert kernel launch");
+    });
+}
+
 pa_status pa_fill_bytes(void* buf, size_t bytes, int value, void* stream) {
     return guarded([&] {
         if (bytes % 16 != 0 || (bytes && !buf)) throw std::invalid_argument("fill_bytes: bad arguments");

@@ -1,8 +1,9 @@
 """MI355X (gfx950) paged flash-decoding: Python side of libpa_decode.so.
 
-`core` mirrors decode.hpp / paged_kv_cache.hpp over the C ABI; `decoder`
-mirrors the reference's torch binding (`Decoder`). Importing this package does
-not load the library; the first call does, and fails loudly if it is missing.
+`core` mirrors decode.hpp / paged_kv_cache.hpp over the C ABI; `Decoder` is
+the reference's torch binding (compiled, `_pa_torch`, with a ctypes twin in
+`decoder`). Importing this package does not load the library; the first call
+does, and fails loudly if it is missing.
 """
 
 from . import _lib
@@ -14,9 +15,12 @@ from .core import (FP16, FP8_E4M3, DecodePlan, DevicePlan, PagePool, PagedKVCach
 
 
 def Decoder(*args, **kwargs):
-    """bindings/torch_decode.cu:14-81 Decoder (imports torch lazily)."""
-    from .decoder import Decoder as _Decoder
-    return _Decoder(*args, **kwargs)
+    """bindings/torch_decode.cu:14-81 Decoder (imports torch lazily): the
+    compiled binding (pa_amd/_pa_torch*.so, built from csrc/pa_torch.cpp) when
+    it was built, else the ctypes one (decoder.Decoder); both drive the same
+    library and kernels."""
+    from .decoder import decoder_class
+    return decoder_class()(*args, **kwargs)
 
 
 __all__ = [

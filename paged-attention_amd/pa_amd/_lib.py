@@ -131,6 +131,8 @@ SIGNATURES: dict[str, tuple] = {
     "pa_stream_read_ex": (_I, [_P, _S, _I, _I, _I, _I, _P, _P]),
     "pa_stream_read_chunked": (_I, [_P, _S, _I, _I, _I, _P, _P]),
     "pa_fill_bytes": (_I, [_P, _S, _I, _P]),
+    "pa_f32_to_f16": (_I, [_P, _P, _S, _P]),
+    "pa_f16_to_f32": (_I, [_P, _P, _S, _P]),
     "pa_pool_create": (_I, [_I, _I, _I, _I, _PP]),
     "pa_pool_destroy": (None, [_P]),
     "pa_pool_admit": (_I, [_P]),

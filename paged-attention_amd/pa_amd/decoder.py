@@ -7,6 +7,10 @@
 
 It runs libpa_decode.so's HIP kernels on the current torch stream. Argument
 checks raise RuntimeError, as TORCH_CHECK does in the reference.
+
+Two implementations: the compiled extension `pa_amd._pa_torch` (csrc/pa_torch.cpp,
+built by build.py's build_torch_ext; the one `pa_amd.Decoder` returns when it
+was built) and this module's ctypes class, which needs no build against torch.
 """
 
 from __future__ import annotations
@@ -118,3 +122,24 @@ class Decoder:
     @property
     def num_segments(self) -> int:
         return len(self._plan.segments) if self._plan is not None else 0
+
+
+_compiled = None
+
+
+def decoder_class():
+    """The compiled binding's Decoder class if its module was built, else this
+    module's ctypes Decoder. A built module that fails to import raises. With
+    PA_DECODE_LIB naming another library build, the ctypes Decoder (the
+    compiled module is linked against the in-tree library)."""
+    global _compiled
+    if _compiled is None:
+        import os
+        from ._lib import PKG_DIR, _init_torch_device_state
+        if "PA_DECODE_LIB" not in os.environ and any((PKG_DIR / "pa_amd").glob("_pa_torch*.so")):
+            _init_torch_device_state()     # torch's HIP state before the library loads
+            from . import _pa_torch
+            _compiled = _pa_torch.Decoder
+        else:
+            _compiled = False
+    return _compiled or Decoder

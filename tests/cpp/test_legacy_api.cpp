@@ -5,8 +5,10 @@
 //
 //   test_legacy_api cpu   host-only: fp16 codec against the oracle's (every
 //                         half, ties, specials), CpuAttention against the
-//                         oracle's cpu_attention and closed forms
-//   test_legacy_api gpu   PagedPool / PagedPoolAttention on the device
+//                         oracle's cpu_attention and closed forms, the pool's
+//                         free sizing helpers
+//   test_legacy_api gpu   PagedPool (decode, decode_device) / PagedPoolAttention
+//                         on the device
 //
 // Exit status 0 = every check passed; each failure prints one line.
 
@@ -159,6 +161,23 @@ void cpu_checks() {
 
 constexpr int kD = 128;
 
+// pool.hpp:63-72's free helpers: closed forms for this pool's element sizes.
+void helper_checks() {
+    expect(paged_waste_tokens(17) == 15 && paged_waste_tokens(16) == 0 && paged_waste_tokens(1) == 15 &&
+               paged_waste_tokens(5, 4) == 3 && paged_waste_tokens(8192, 8192) == 0,
+           "paged_waste_tokens closed forms");
+    const size_t gib = size_t{1} << 30;
+    // 1 GiB of fp16 pages of 16 x 128: 2 * 2 * 16 * 128 = 8 KiB per page, 131072
+    // pages; 1024 tokens = 64 pages per sequence.
+    expect(paged_max_sequences_for_budget(gib, 1024, 128) == 2048, "budget helper, fp16");
+    expect(paged_max_sequences_for_budget(gib, 1024, 128, 16, decode::KVDtype::FP8_E4M3) == 4096,
+           "budget helper, FP8 (one byte per element)");
+    expect(paged_max_sequences_for_budget(gib, 1025, 128) == 131072 / 65, "budget helper rounds pages up");
+    expect(paged_max_sequences_for_budget(1000, 16, 128) == 0, "a budget below one page holds no sequence");
+    expect_throw<std::invalid_argument>([] { paged_max_sequences_for_budget(1 << 20, 0, 128); },
+                                        "budget helper rejects a zero length");
+}
+
 void gpu_checks() {
     CpuAttention       cpu;
     PagedPoolAttention paged;
@@ -245,6 +264,46 @@ void gpu_checks() {
             [&] { pool.append_token(slot, 4 * PAGE_SIZE, in.K.data(), in.V.data()); }, "append_token without a page");
         expect(pool.actual_len(slot) == 4 * PAGE_SIZE, "a refused append_token changes nothing");
     }
+    // decode_device (pool.hpp:21-24): fp32 device q / out, the first actual_len
+    // rows of a slot, no synchronization. Whole length: bitwise equal to
+    // decode(); a prefix: bitwise equal to a pool holding only the prefix.
+    {
+        const int T = 300, Tp = 129;
+        PagedPool pool(64, 3, 32, kD);
+        const Inputs in = make_inputs(kD, T, 77), other = make_inputs(kD, T, 78);
+        const int s_other = pool.admit(other.K.data(), other.V.data(), T);
+        const int slot = pool.admit(in.K.data(), in.V.data(), T);
+        expect(s_other >= 0 && slot >= 0 && slot != s_other, "two slots for decode_device");
+        float *dq = nullptr, *dout = nullptr;
+        HIP_CHECK(hipMalloc(&dq, sizeof(float) * kD));
+        HIP_CHECK(hipMalloc(&dout, sizeof(float) * 2 * kD));
+        HIP_CHECK(hipMemcpy(dq, in.q.data(), sizeof(float) * kD, hipMemcpyHostToDevice));
+        pool.decode_device(slot, T, dq, dout);
+        pool.decode_device(slot, Tp, dq, dout + kD, nullptr, nullptr, nullptr);
+        HIP_CHECK(hipDeviceSynchronize());
+        std::vector<float> whole(kD), prefix(kD), host(kD), ref_prefix(kD), ref(kD);
+        HIP_CHECK(hipMemcpy(whole.data(), dout, sizeof(float) * kD, hipMemcpyDeviceToHost));
+        HIP_CHECK(hipMemcpy(prefix.data(), dout + kD, sizeof(float) * kD, hipMemcpyDeviceToHost));
+        pool.decode(slot, in.q.data(), host.data());
+        expect(whole == host, "decode_device over the whole slot == decode (bitwise)");
+        PagedPool small(16, 1, 16, kD);
+        const int sp = small.admit(in.K.data(), in.V.data(), Tp);
+        small.decode(sp, in.q.data(), ref_prefix.data());
+        expect(prefix == ref_prefix, "decode_device over a prefix == a pool of the prefix (bitwise)");
+        const auto q16 = round_f16(in.q), K16 = round_f16(in.K), V16 = round_f16(in.V);
+        CpuAttention().run(q16.data(), K16.data(), V16.data(), ref.data(), Tp, kD);
+        expect(max_abs(prefix, ref) < 2e-3, "decode_device prefix vs cpu");
+        expect_throw<std::invalid_argument>([&] { pool.decode_device(slot, T + 1, dq, dout); },
+                                            "decode_device past the slot's length");
+        expect_throw<std::invalid_argument>([&] { pool.decode_device(slot, 0, dq, dout); }, "decode_device of 0 rows");
+        expect_throw<std::invalid_argument>([&] { pool.decode_device(2, 1, dq, dout); }, "decode_device of a free slot");
+        // The device pools: distinct, V laid out after K.
+        const auto* kb = static_cast<const unsigned char*>(pool.kv_K_base());
+        const auto* vb = static_cast<const unsigned char*>(pool.kv_V_base());
+        expect(kb && vb && vb >= kb + pool.total_kv_bytes() / 2, "kv_K_base / kv_V_base");
+        HIP_CHECK(hipFree(dq));
+        HIP_CHECK(hipFree(dout));
+    }
     // An FP8 pool: E4M3 of the fp16-rounded rows times 1/scale; compared with
     // fp32 attention over the same quantized values.
     {
@@ -271,6 +330,7 @@ int main(int argc, char** argv) {
     const std::string mode = argc > 1 ? argv[1] : "cpu";
     try {
         cpu_checks();
+        helper_checks();
         if (mode == "gpu") gpu_checks();
     } catch (const std::exception& e) {
         std::printf("FAIL: unexpected exception: %s\n", e.what());

@@ -109,3 +109,19 @@ def test_append_rejects_thread_counts_past_int32():
     assert b"INT_MAX" in lib.pa_last_error()
     assert lib.pa_append_quantize(1, None, None, None, None, None, 0, limit, hkv, 128, 16, 1.0, 1.0, None) \
         == _lib.PA_ERR_INVALID_ARGUMENT
+
+
+def test_compiled_torch_binding_loads_without_a_device():
+    """The compiled binding (pa_amd/_pa_torch*.so, built with the library) is
+    in tree, imports, exposes the reference binding's Decoder surface and
+    raises RuntimeError for a bad seq_lens tensor before any device use."""
+    import torch
+    from pa_amd.decoder import decoder_class
+    from pa_amd import _pa_torch
+    assert decoder_class() is _pa_torch.Decoder
+    dec = _pa_torch.Decoder(32, 8, 128, 16, False)
+    for name in ("plan", "run", "num_ctas", "num_segments"):
+        assert hasattr(dec, name)
+    assert dec.num_ctas == 0 and dec.num_segments == 0
+    with pytest.raises(RuntimeError, match="CPU int32"):
+        dec.plan(torch.tensor([10], dtype=torch.int64))

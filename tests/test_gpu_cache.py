@@ -282,3 +282,31 @@ def test_decoder_plan_while_previous_run_is_queued():
     torch.cuda.synchronize()
     assert torch.equal(out_a.view(torch.int16), ref_a.view(torch.int16))
     assert torch.equal(out_b.view(torch.int16), ref_b.view(torch.int16))
+
+
+def test_f32_f16_conversions():
+    """pa_f32_to_f16 rounds to nearest even (the oracle's encoder, every fp16
+    value, the midpoints between neighbours and one ulp either side, specials);
+    pa_f16_to_f32 is exact for all 65536 codes."""
+    import torch
+    from pa_amd._lib import load
+    lib = load()
+    codes = np.arange(65536, dtype=np.uint16)
+    h = to_device(codes)
+    f = torch.empty(65536, dtype=torch.float32, device="cuda")
+    assert lib.pa_f16_to_f32(h.data_ptr(), f.data_ptr(), 65536, None) == 0
+    torch.cuda.synchronize()
+    want = oracle.f16_bits_to_f32(codes)
+    got = f.cpu().numpy()
+    same = (got.view(np.uint32) == want.view(np.uint32)) | (np.isnan(got) & np.isnan(want))
+    assert same.all()
+    v = oracle.f16_bits_to_f32(np.arange(0x7c00, dtype=np.uint16))
+    mid = ((v[:-1].astype(np.float64) + v[1:]) / 2).astype(np.float32)
+    x = np.concatenate([v, mid, np.nextafter(mid, np.float32(np.inf)), np.nextafter(mid, np.float32(0)),
+                        [65504.0, 65519.0, 65520.0, 1e9, np.inf, 5.9e-8, 3e-8, 2.9e-8, 0.0]]).astype(np.float32)
+    x = np.concatenate([x, -x])
+    xd = torch.from_numpy(x).cuda()
+    o = torch.empty(x.size, dtype=torch.int16, device="cuda")
+    assert lib.pa_f32_to_f16(xd.data_ptr(), o.data_ptr(), x.size, None) == 0
+    torch.cuda.synchronize()
+    assert np.array_equal(o.cpu().numpy().view(np.uint16), oracle.f32_to_f16_bits(x))

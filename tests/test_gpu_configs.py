@@ -114,6 +114,32 @@ def test_alloc_kv_pools_decode_bitwise_equal(fp8):
     torch.cuda.synchronize()
     assert torch.equal(a.view(torch.int16), b.view(torch.int16))
 
+@pytest.mark.parametrize("fp8", DTYPES, ids=IDS)
+def test_compiled_and_ctypes_decoders_agree(fp8):
+    """pa_amd.Decoder is the compiled binding (csrc/pa_torch.cpp); the ctypes
+    Decoder drives the same library: same plans, bitwise the same outputs,
+    RuntimeError for the same bad inputs."""
+    import torch
+    from pa_amd import decoder as ctypes_decoder
+    from pa_amd._pa_torch import Decoder as Compiled
+    lens = [1024, 3, 5000, 77]
+    q, k, v, table, ks, vs = paged_inputs(len(lens), lens, 32, 8, 16, fp8, seed=31)
+    t = torch.tensor(lens, dtype=torch.int32)
+    outs = []
+    for cls in (Compiled, ctypes_decoder.Decoder):
+        dec = cls(32, 8, D, 16, fp8)
+        dec.plan(t, 0)
+        outs.append((dec.run(q, k, v, table, t.cuda(), ks, vs), dec.num_ctas, dec.num_segments))
+        with pytest.raises(RuntimeError):
+            dec.run(q[:1].contiguous(), k, v, table, t.cuda(), ks, vs)
+        with pytest.raises(RuntimeError):
+            dec.plan(t.long())
+    torch.cuda.synchronize()
+    assert isinstance(pa_amd.Decoder(32, 8, D, 16, fp8), Compiled)
+    assert outs[0][1:] == outs[1][1:]
+    assert torch.equal(outs[0][0].view(torch.int16), outs[1][0].view(torch.int16))
+
+
 def test_decoder_rejects_inconsistent_inputs():
     """Decoder.run raises RuntimeError (the reference's TORCH_CHECK) for inputs
     whose shapes or types do not match the plan, before any launch."""
