@@ -30,8 +30,10 @@ Fields of the JSON line:
                warm-up steps alone do not: C2 162-163 us against 157-159 us
                per step)
   workloads    the same figures (step, split kernel, cold) for C1, C3 (the
-               FP8 target), C2 at one page per sequence, C5 fp16 and FP8,
-               timed in the same run; paging_overhead = C2 at 16-token pages
+               FP8 target), C2 at 16-token pages and at one page per
+               sequence, C5 fp16 and FP8,
+               timed in the same run (each over max(K, 100) steps after
+               max(W, 20) warm-ups); paging_overhead = C2 at 16-token pages
                against one page per sequence; targets = the goals the
                north star states, checked on these figures
   cpu_baseline the reference's cpu_attention (compiled from its source into
@@ -314,10 +316,12 @@ def device_report() -> dict:
 
 
 # Workloads timed beside the headline one (their figures go under
-# "workloads"): the CPU-runnable C1, the FP8 target C3, the contiguous end of
-# C2's page-size sweep (paging overhead = C2 at 16-token pages against one page
-# per sequence) and C5 in both dtypes. (key, config, page size)
-EXTRA = [("c1", "c1", 16), ("c3", "c3", 16), ("c2_p8192", "c2", 8192), ("c5", "c5", 16), ("c5fp8", "c5fp8", 16)]
+# "workloads"): the CPU-runnable C1, the FP8 target C3, both ends of C2's
+# page-size comparison (paging overhead = C2 at 16-token pages against one
+# page per sequence, both timed the same way) and C5 in both dtypes.
+# (key, config, page size)
+EXTRA = [("c1", "c1", 16), ("c3", "c3", 16), ("c2_p16", "c2", 16), ("c2_p8192", "c2", 8192), ("c5", "c5", 16),
+         ("c5fp8", "c5fp8", 16)]
 
 
 def workload_figures(s, desc: str, steps: int, warmup: int, cold_iters: int, flusher) -> dict:
@@ -499,22 +503,25 @@ def main() -> None:
         result["workloads"] = {}
         headline = (args.config, args.page_size)
         for key, cfg, page in EXTRA:
-            if (cfg, page) == headline:
+            if (cfg, page) == headline and key != "c2_p16":
                 continue
             d = CONFIGS[cfg][0] if page == 16 else f"{CONFIGS[cfg][0].split(',')[0]}, {CONFIGS[cfg][0].split(', ')[1]}, {page}-token pages (one page per sequence)"
             print(f"# workload {key}: {d}", file=sys.stderr, flush=True)
             kept[key] = bd.Setup(seq_lens_of(cfg), HQ, HKV, D, page, CONFIGS[cfg][4], shuffle=True, ctas=args.ctas)
-            result["workloads"][key] = workload_figures(kept[key], d, args.steps, args.warmup,
+            # Each is timed over at least 100 steps after 20 warm-ups (K and W
+            # count the headline's steps; a short window reads a few percent
+            # slow while a new workload's first launches settle).
+            result["workloads"][key] = workload_figures(kept[key], d, max(args.steps, 100), max(args.warmup, 20),
                                                         min(args.cold_iters, 20), fl)
         w = result["workloads"]
-        if args.config == "c2" and args.page_size == 16 and "c2_p8192" in w:
-            c = w["c2_p8192"]
+        if "c2_p16" in w and "c2_p8192" in w:
+            a, c = w["c2_p16"], w["c2_p8192"]
             result["paging_overhead"] = {
                 "page_size": 16, "against_page_size": 8192,
-                "step_pct": round(100 * (result["us_per_step"] / c["us_per_step"] - 1), 2),
-                "split_pct": round(100 * (result["roofline"]["avg_us"] / c["split_us"] - 1), 2),
-                "cold_pct": (round(100 * (result["cold"]["us_median"] / c["cold_us"] - 1), 2)
-                             if "cold" in result and "cold_us" in c else None)}
+                "step_pct": round(100 * (a["us_per_step"] / c["us_per_step"] - 1), 2),
+                "split_pct": round(100 * (a["split_us"] / c["split_us"] - 1), 2),
+                "cold_pct": (round(100 * (a["cold_us"] / c["cold_us"] - 1), 2)
+                             if "cold_us" in a and "cold_us" in c else None)}
         if args.config == "c2" and args.page_size == 16:
             result["targets"] = {
                 "c2_fp16_step_ge_80pct": result["pct_of_peak"] >= 80.0,
