@@ -1,4 +1,4 @@
-"""The BASELINE configurations through the torch `Decoder` binding
+"""The five benchmark configurations (C1-C5) through the torch `Decoder` binding
 (bindings/torch_decode.cu:14-81): C1-C5 at full size against the oracle,
 config 2's page-size sweep at full size (bitwise equal across page sizes, the
 contiguous point against the oracle), config 3's stored FP8 bytes at its own
@@ -23,25 +23,25 @@ IDS = ["fp16", "fp8"]
 
 @pytest.mark.parametrize("fp8", DTYPES, ids=IDS)
 def test_decoder_binding_config1(fp8):
-    """BASELINE config 1 shape (4 x 1024, P=16, scattered) via the torch_decode
+    """Config C1 shape (4 x 1024, P=16, scattered) via the torch_decode
     `Decoder` signature."""
     err, dec = decoder_case(4, [1024] * 4, fp8)
     assert dec.num_ctas > 0 and dec.num_segments >= 32
     assert err < TOL, err
 
 def test_decoder_full_size_config2():
-    """BASELINE config 2 at full size: 32 x 8192 fp16, 16-token scattered pages."""
+    """Config C2 at full size: 32 x 8192 fp16, 16-token scattered pages."""
     err, _ = decoder_case(32, [8192] * 32, False, threads=16)
     assert err < TOL, err
 
 def test_decoder_full_size_config3():
-    """BASELINE config 3 at full size: 64 x 8192, FP8 E4M3 (amax/448 scales,
+    """Config C3 at full size: 64 x 8192, FP8 E4M3 (amax/448 scales,
     quantized by the append kernel), 16-token scattered pages."""
     err, _ = decoder_case(64, [8192] * 64, True, threads=16)
     assert err < TOL, err
 
 def test_decoder_full_size_config4_all_rows():
-    """BASELINE config 4 at full size (128 ragged rows, L ~ U[128, 16384],
+    """Config C4 at full size (128 ragged rows, L ~ U[128, 16384],
     seed 4, about 4.3 GB of KV) decoded in one batch; every row against the
     oracle. Rows split across blocks go through the merge kernel."""
     rng = np.random.default_rng(4)
@@ -51,20 +51,20 @@ def test_decoder_full_size_config4_all_rows():
     assert err < TOL, err
 
 def test_decoder_ragged_config4_subset():
-    """BASELINE config 4's ragged lengths (U[128, 16384] from a seed), first 16 rows."""
+    """Config C4's ragged lengths (U[128, 16384] from a seed), first 16 rows."""
     rng = np.random.default_rng(4)
     lens = [int(x) for x in rng.integers(128, 16385, size=16)]
     err, _ = decoder_case(len(lens), lens, False, threads=16)
     assert err < TOL, err
 
 def test_decoder_long_context_config5_fp16():
-    """BASELINE config 5 (1 x 131072), fp16 KV."""
+    """Config C5 (1 x 131072), fp16 KV."""
     err, dec = decoder_case(1, [131072], False, threads=8)
     assert dec.num_segments > 8 * 64
     assert err < TOL, err
 
 def test_decoder_long_context_config5_fp8():
-    """BASELINE config 5 (1 x 131072), FP8 KV: hundreds of splits per row."""
+    """Config C5 (1 x 131072), FP8 KV: hundreds of splits per row."""
     err, dec = decoder_case(1, [131072], True, threads=8)
     assert dec.num_segments > 8 * 64
     assert err < TOL, err
