@@ -162,8 +162,11 @@ pa_status pa_decode_merge(int dtype, const pa_decode_params* p, void* stream);
  * that forbid hipMalloc): the same split and merge launches, but the partial
  * workspace of rows split across blocks lives in a fixed 32 MiB device array
  * of the library (one per GPU, held until the process ends) instead of
- * p->partial_out / p->partial_lse, which are ignored. num_segments is the
- * plan's segment count (pa_plan_num_segments); a plan whose workspace,
+ * p->partial_out / p->partial_lse, which are ignored. num_segments must be
+ * the bound plan's segment count (pa_plan_num_segments): the kernels write
+ * that many partials, so a smaller count would let them write past the array
+ * (counts below batch * num_kv_heads or p->max_item_segments are refused with
+ * PA_ERR_INVALID_ARGUMENT); a plan whose workspace,
  * num_segments * group * (head_dim + 1) * 4 bytes, exceeds 32 MiB is refused
  * with PA_ERR_LENGTH (plans merged in the split kernel, p->block_merge = 1,
  * need none). Allocates nothing. Calls on one GPU share its array: calls that

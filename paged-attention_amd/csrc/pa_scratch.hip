@@ -66,7 +66,12 @@ pa_status pa_decode_static(int dtype, const pa_decode_params* p, int num_segment
         if (p->num_kv_heads <= 0 || p->num_q_heads <= 0 || p->num_q_heads % p->num_kv_heads != 0)
             throw std::invalid_argument("num_q_heads must be a multiple of num_kv_heads");
         if (p->head_dim != pa::kHeadDim) throw std::invalid_argument("unsupported head_dim " + std::to_string(p->head_dim));
-        if (num_segments < 0 || (p->num_ctas > 0 && num_segments == 0))
+        // The kernels write one partial per split segment of the bound plan,
+        // which only the caller knows here; reject counts no plan can have
+        // (every (row, kv head) holds at least one segment, no row more than
+        // the plan's most).
+        const long items = static_cast<long>(p->batch) * p->num_kv_heads;
+        if (num_segments < 0 || (p->num_ctas > 0 && (num_segments < items || num_segments < p->max_item_segments)))
             throw std::invalid_argument("decode_static: num_segments must be the plan's segment count");
         const size_t group = static_cast<size_t>(p->num_q_heads / p->num_kv_heads);
         const size_t rows  = static_cast<size_t>(num_segments) * group;

@@ -39,9 +39,11 @@ def _params(q, k, v, table, lens, hq, hkv, ks, vs, dplan):
 
 def test_decode_static_refuses_oversized_plans_without_a_device():
     """A plan whose partial workspace exceeds the 32 MiB array is refused with
-    PA_ERR_LENGTH, and null params, a zero segment count for a non-empty grid,
-    an unknown dtype or an unsupported head_dim with PA_ERR_INVALID_ARGUMENT,
-    before the library looks up the array or launches anything."""
+    PA_ERR_LENGTH, and null params, a segment count no plan of the params can
+    have (zero for a non-empty grid, fewer than batch x kv heads, fewer than the
+    plan's most per row), an unknown dtype or an unsupported head_dim with
+    PA_ERR_INVALID_ARGUMENT, before the library looks up the array or launches
+    anything."""
     lib = _lib.load()
     p = pa_amd.DecodeParams()
     p.num_q_heads, p.num_kv_heads, p.head_dim, p.num_ctas, p.batch = 32, 8, D, 2048, 4
@@ -51,6 +53,10 @@ def test_decode_static_refuses_oversized_plans_without_a_device():
     assert b"static scratch" in lib.pa_last_error()
     assert lib.pa_decode_static(0, None, 10, None) == _lib.PA_ERR_INVALID_ARGUMENT
     assert lib.pa_decode_static(0, ctypes.byref(p), 0, None) == _lib.PA_ERR_INVALID_ARGUMENT
+    assert lib.pa_decode_static(0, ctypes.byref(p), 31, None) == _lib.PA_ERR_INVALID_ARGUMENT   # < 4 x 8 rows
+    p.max_item_segments = 64
+    assert lib.pa_decode_static(0, ctypes.byref(p), 40, None) == _lib.PA_ERR_INVALID_ARGUMENT   # < one row's
+    p.max_item_segments = 0
     assert lib.pa_decode_static(5, ctypes.byref(p), 10, None) == _lib.PA_ERR_INVALID_ARGUMENT
     p.head_dim = 64
     assert lib.pa_decode_static(0, ctypes.byref(p), 10, None) == _lib.PA_ERR_INVALID_ARGUMENT
