@@ -6,8 +6,9 @@
 // Split kernel design (one wave64 = one work unit of the persistent plan):
 //   * A wave streams its own contiguous list of (row, kv head, token range)
 //     segments in steps of NG = 16 or 32 tokens (two 16-token halves), DEPTH
-//     steps of K/V in flight in registers. The pages of a step are looked up
-//     another DEPTH steps ahead, so an HBM load never waits on the block table.
+//     steps of K/V in flight (in registers, or in the LDS stage below). The
+//     pages of a step are looked up another DEPTH steps ahead, so an HBM load
+//     never waits on the block table.
 //   * K is held token-major: in each 16-token half, lane (c, kb) holds token
 //     c and a quarter of its dims. That is the A-operand layout of
 //     v_mfma_f32_16x16x32_f16 for S^T = K Q^T with the G query heads sharing
@@ -21,18 +22,23 @@
 //   * fp16 loads K and V straight into those layouts. FP8 rows are 128 B, so
 //     the same layouts would split every row over many lanes' small pieces;
 //     the FP8 kernel instead loads each 16-token half fully coalesced (16 B
-//     per lane, 8 whole rows per instruction) and moves it into the layouts
-//     through a per-wave LDS stage whose 16-byte chunks are XOR-swizzled by
-//     row, so both the row-wise writes and the column-wise K reads are free
-//     of bank conflicts.
+//     per lane, 8 whole rows per instruction) straight into a per-wave LDS
+//     stage (LDS-destination buffer loads, one step in flight) and reads the
+//     layouts from there. The stage's 16-byte chunks are XOR-swizzled by row
+//     (the swizzle is applied to the source addresses, since lane i's bytes
+//     land at 16 i), so the column-wise K reads are free of bank conflicts.
 //   * When the page size is a power of two >= 16, a 16-token half lies in one
-//     page: one wave-uniform scalar lookup per half, and each load is a raw
+//     page: one wave-uniform table read per half, and each load is a raw
 //     buffer load from an SGPR resource based at the half's first row, with
 //     constant lane offsets. The resource's range is the half's valid tokens,
 //     so loads past a segment's end (and every load of a slot past the unit's
 //     last step) return zeros without touching memory, and every slot issues
-//     the same loads, which keeps the hardware wait counts exact. Other page
-//     sizes resolve pages per lane with plain loads.
+//     the same loads, which keeps the hardware wait counts exact. Smaller
+//     pages go through the LDS stage for both element types: pages of whole
+//     1 KiB parts (fp16 P = 4 and 8, FP8 P = 8) with one resource per part,
+//     any other size with each lane loading a row whose page it looks up
+//     itself (the step's table entries spread over the lanes, handed out by
+//     ds_bpermute).
 //   * Online softmax in base 2 with a lazy running max: probabilities use a
 //     reference max per head that only moves (with the exact O/l rescale) when
 //     a score exceeds it by more than 2^8, so the cross-lane max reduction is
