@@ -109,3 +109,49 @@ def test_decode_static_matches_decode_on_two_calls(fp8):
                                   np.asarray(lens, np.int32), hq, hkv, D, 16, ks, vs, threads=16)
         err = float(np.max(np.abs(out_st.float().cpu().numpy() - ref)))
         assert err < TOL, (i, err)
+
+
+@pytest.mark.gpu
+@pytest.mark.usefixtures("gpu_device")
+def test_decode_static_graph_replays_match_eager():
+    """The callers the entry point is for: pa_decode_static captured into a HIP
+    graph, on a plan whose rows span blocks (the merge kernel reads the
+    library's array). Every replay, with q rewritten before it and an eager
+    pa_decode_static of other inputs after it (the same array, the same
+    stream), equals an eager pa_decode of the same q with the plan's own
+    workspace, bitwise."""
+    import torch
+    lib = _lib.load()
+    hq, hkv = 32, 8
+    lens = [1024] * 4
+    q, k, v, table, ks, vs = paged_inputs(len(lens), lens, hq, hkv, 16, False, seed=77)
+    plan = pa_amd.make_plan(pa_amd.FP16, lens, hq, hkv, D, 0)
+    nseg = len(plan.segments)
+    dplan = pa_amd.DevicePlan()
+    dplan.upload(plan, hq // hkv, D)
+    p_ref, out_ref = _params(q, k, v, table, lens, hq, hkv, ks, vs, dplan)
+    assert p_ref.needs_merge == 1 and p_ref.block_merge == 0
+    p_st, out_st = _params(q, k, v, table, lens, hq, hkv, ks, vs, dplan)
+    g = torch.Generator(device="cuda").manual_seed(5)
+    other_q = torch.randn(q.shape, device="cuda", dtype=q.dtype, generator=g)
+    p_other, _ = _params(other_q, k, v, table, lens, hq, hkv, ks, vs, dplan)
+    st = torch.cuda.Stream()
+    with torch.cuda.stream(st):
+        h = st.cuda_stream
+        # Eager first: the array's address is looked up outside the capture.
+        assert lib.pa_decode_static(0, ctypes.byref(p_st), nseg, h) == _lib.PA_OK, lib.pa_last_error()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=st):
+            status = lib.pa_decode_static(0, ctypes.byref(p_st), nseg, torch.cuda.current_stream().cuda_stream)
+        assert status == _lib.PA_OK, lib.pa_last_error()
+        torch.cuda.synchronize()
+        for rep in range(4):
+            q.normal_(generator=g)
+            assert lib.pa_decode(0, ctypes.byref(p_ref), h) == _lib.PA_OK
+            torch.cuda.synchronize()
+            out_st.zero_()
+            graph.replay()
+            assert lib.pa_decode_static(0, ctypes.byref(p_other), nseg, h) == _lib.PA_OK
+            torch.cuda.synchronize()
+            assert torch.equal(out_st.view(torch.int16), out_ref.view(torch.int16)), f"replay {rep} differs"
