@@ -245,3 +245,26 @@ def test_full_size_config3_stored_fp8_bytes():
             assert np.array_equal(got, want), f"row {b}: stored FP8 bytes differ"
             saturated += int(np.count_nonzero((want & 0x7f) == 0x7e))
     assert saturated >= 2                                          # each tensor's amax lands on +-448
+
+
+@pytest.mark.parametrize("compiled", [True, False], ids=["compiled", "ctypes"])
+def test_decoder_empty_batch(compiled):
+    """An empty batch (no sequences) plans to zero work units and segments and
+    decodes to an empty output without a launch or an error, through both
+    Decoder classes (the reference's make_plan and paged_decode do no work
+    for it)."""
+    import torch
+    from pa_amd.decoder import Decoder as CtypesDecoder, decoder_class
+    cls = decoder_class() if compiled else CtypesDecoder
+    if compiled and cls is CtypesDecoder:
+        pytest.skip("the compiled binding is not built")
+    dec = cls(32, 8, 128, 16, False)
+    dec.plan(torch.zeros(0, dtype=torch.int32))
+    assert dec.num_ctas == 0 and dec.num_segments == 0
+    q = torch.empty(0, 32, 128, dtype=torch.float16, device="cuda")
+    kv = torch.zeros(1, 8, 16, 128, dtype=torch.float16, device="cuda")
+    table = torch.zeros(0, 1, dtype=torch.int32, device="cuda")
+    lens = torch.zeros(0, dtype=torch.int32, device="cuda")
+    out = dec.run(q, kv, kv, table, lens, 1.0, 1.0)
+    torch.cuda.synchronize()
+    assert out.shape == (0, 32, 128) and out.dtype == torch.float16
