@@ -310,3 +310,28 @@ def test_f32_f16_conversions():
     assert lib.pa_f32_to_f16(xd.data_ptr(), o.data_ptr(), x.size, None) == 0
     torch.cuda.synchronize()
     assert np.array_equal(o.cpu().numpy().view(np.uint16), oracle.f32_to_f16_bits(x))
+
+
+def test_cache_plan_and_run_of_no_slots():
+    """PagedKVCache::plan of an empty slot list and PagedKVCache::decode of
+    batch 0 (paged_kv_cache.cu:157-210 with no rows): a plan of zero work
+    units and segments, and run / decode return without a launch or an error,
+    also right after a non-empty decode on the same cache."""
+    import torch
+    hq, hkv = 32, 8
+    cache = pa_amd.PagedKVCache(8, 16, hkv, D, 2, 4, pa_amd.FP16)
+    q0 = torch.empty(0, hq, D, dtype=torch.float16, device="cuda")
+    out0 = torch.empty_like(q0)
+    cache.plan([], hq)
+    assert cache.last_plan().num_ctas == 0 and len(cache.last_plan().segments) == 0
+    cache.run(q0, out0)
+    s_ = cache.admit()
+    k = torch.randn(20, hkv, D, dtype=torch.float16, device="cuda")
+    assert cache.append(s_, k, k, 20)
+    q = torch.randn(1, hq, D, dtype=torch.float16, device="cuda")
+    out = torch.empty_like(q)
+    cache.decode(q, out, 1, hq)
+    cache.decode(q0, out0, 0, hq)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all()
+    cache.close()
