@@ -92,15 +92,18 @@ def test_output_invariant_under_page_placement(fp8):
 
 @pytest.mark.parametrize("case", range(24))
 def test_seeded_random_configurations(case):
-    """24 seeded random combinations of dtype, GQA shape, page size, batch,
-    lengths (1 .. 3000), grid size and append chunking through the cache,
-    each against the oracle (bytes bit-exact, output within TOL)."""
+    """24 seeded random combinations of dtype, GQA shape (groups 1 to 8), page
+    size (1 to 1024, powers of two and not), batch, lengths (1 .. 6000), grid
+    size (one unit to more than one resident wave) and append chunking (per
+    slot or batched) through the cache, each against the oracle (bytes
+    bit-exact, output within TOL)."""
     rng = np.random.default_rng(1000 + case)
     fp8 = bool(rng.integers(0, 2))
-    hq, hkv = [(8, 8), (8, 4), (16, 4), (32, 8), (8, 1), (32, 4)][int(rng.integers(0, 6))]
-    page = int(rng.choice([1, 2, 3, 4, 5, 8, 16, 32, 64, 128]))
-    lens = [int(x) for x in rng.integers(1, 3001, size=int(rng.integers(1, 9)))]
-    ctas = int(rng.choice([0, 0, 1, 3, 17, 300]))
+    shapes = [(8, 8), (8, 4), (16, 4), (32, 8), (8, 1), (32, 4), (64, 8), (16, 2), (2, 1)]
+    hq, hkv = shapes[int(rng.integers(0, len(shapes)))]
+    page = int(rng.choice([1, 2, 3, 4, 5, 7, 8, 12, 16, 32, 64, 128, 256, 1024]))
+    lens = [int(x) for x in rng.integers(1, 6001, size=int(rng.integers(1, 9)))]
+    ctas = int(rng.choice([0, 0, 1, 3, 17, 300, 2048, 3000]))
     chunk = int(rng.choice([0, 0, 7, 64]))
     err, _, plan = run_cache_case(fp8, hq, hkv, page, lens, num_ctas=ctas, chunk=chunk, seed=case,
                                   shuffle_seed=case, batched=bool(rng.integers(0, 2)))
