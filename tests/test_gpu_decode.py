@@ -312,3 +312,37 @@ def test_graph_capture_replays_match_eager(lens):
             assert torch.equal(out, ref), f"replay {rep} differs"
     assert cache.last_plan().num_ctas > 0
     cache.close()
+
+
+@pytest.mark.parametrize("fp8", DTYPES, ids=IDS)
+def test_decoders_on_concurrent_streams_match_alone(fp8):
+    """Three Decoders with different plans (32 x 2048: split rows merged in
+    the split kernel; 4 x 1024 and a ragged batch: through the merge kernel)
+    launched on three streams at once, five steps each with no
+    synchronization between them: every output equals the same decoder's
+    output when it runs alone, bitwise. Decoders share no device state (each
+    has its own device plan and partial workspace)."""
+    import torch
+    cases = [([2048] * 32, 5), ([1024] * 4, 6), ([3000, 17, 9000], 7)]
+    decs, args, alone = [], [], []
+    for lens, seed in cases:
+        q, k, v, table, ks, vs = paged_inputs(len(lens), lens, 32, 8, 16, fp8, seed)
+        dec = pa_amd.Decoder(32, 8, D, 16, fp8)
+        lt = torch.tensor(lens, dtype=torch.int32)
+        dec.plan(lt, 0)
+        a = (q, k, v, table, lt.cuda(), ks, vs)
+        alone.append(dec.run(*a))
+        decs.append(dec)
+        args.append(a)
+    torch.cuda.synchronize()
+    assert decs[0].num_segments > 32 * 8 and decs[1].num_segments > 4 * 8   # split rows in both
+    streams = [torch.cuda.Stream() for _ in cases]
+    outs = [[] for _ in cases]
+    for _ in range(5):
+        for i, st in enumerate(streams):
+            with torch.cuda.stream(st):
+                outs[i].append(decs[i].run(*args[i]))
+    torch.cuda.synchronize()
+    for i, lens_seed in enumerate(cases):
+        for n, o in enumerate(outs[i]):
+            assert torch.equal(o, alone[i]), f"decoder {i} {lens_seed[0][:3]} step {n} differs"
