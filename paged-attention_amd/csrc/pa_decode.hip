@@ -28,13 +28,13 @@
 //     (the swizzle is applied to the source addresses, since lane i's bytes
 //     land at 16 i), so the column-wise K reads are free of bank conflicts.
 //   * When the page size is a power of two >= 16, a 16-token half lies in one
-//     page: one wave-uniform table read per half (a scalar load), and each
-//     load is a raw
-//     buffer load from an SGPR resource based at the half's first row, with
-//     constant lane offsets. The resource's range is the half's valid tokens,
-//     so loads past a segment's end (and every load of a slot past the unit's
-//     last step) return zeros without touching memory, and every slot issues
-//     the same loads, which keeps the hardware wait counts exact. Smaller
+//     page: one wave-uniform table read (a scalar load) per half, and each
+//     load is a raw buffer load from an SGPR resource based at the half's
+//     first row, with constant lane offsets. The resource's range is the
+//     half's valid tokens, so loads past a segment's end (and every load of a
+//     slot past the unit's last step) return zeros without touching memory,
+//     and every slot issues the same loads, which keeps the hardware wait
+//     counts exact. Smaller
 //     pages go through the LDS stage for both element types: pages of whole
 //     1 KiB parts (fp16 P = 4 and 8, FP8 P = 8) with one resource per part,
 //     any other size with each lane loading a row whose page it looks up
@@ -125,14 +125,6 @@
 #ifndef PA_LDS_DMA
 #define PA_LDS_DMA 1
 #endif
-// Steps in flight on the LDS-destination stage (1 or 2; 2 only for up to four
-// query heads per kv head): each step has its own stage slot per wave, and a
-// step's rows are read once that step's loads have returned, while the next
-// step's loads stay in flight. Two steps measured slower for FP8 (64 x 8192:
-// 165.4 against 163.2 us per step; 1 x 131072: 47.0 against 46.05 us).
-#ifndef PA_DMA_DEPTH
-#define PA_DMA_DEPTH 1
-#endif
 
 namespace pa {
 namespace {
@@ -155,48 +147,24 @@ template <int EB> struct Tune {
 static_assert(Tune<2>::step == 16 || Tune<2>::step == 32, "fp16 step must be 16 or 32");
 static_assert(Tune<1>::step == 16 || Tune<1>::step == 32, "fp8 step must be 16 or 32");
 constexpr bool kLdsDma = PA_LDS_DMA != 0;
-constexpr int  kDmaDepth = PA_DMA_DEPTH;
-static_assert(kDmaDepth == 1 || kDmaDepth == 2, "the LDS-destination stage holds one or two steps");
 
 // LDS-destination load of 16 bytes per lane: lane i's bytes land at dst + 16 i
-// (AUX: the cache-policy operand, 2 = non-temporal). Written as inline
-// assembly: for the builtin form the compiler makes every later LDS read wait
-// for all LDS-destination loads in flight (vmcnt(0)), which would drain the
-// second stage slot before each step. The kernel orders the stage itself:
-// `s_waitcnt vmcnt(n)` before a slot's reads, and the compiler, not knowing
-// these loads, only ever waits for more of them than it needs.
-__device__ __forceinline__ uint32_t lds_m0(u32x4* dst) {
-    return __builtin_amdgcn_readfirstlane(
-        static_cast<uint32_t>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) void*)dst)));
-}
+// (AUX: the cache-policy operand, 2 = non-temporal).
 template <int AUX>
 __device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t rs, u32x4* dst, int voffset) {
-    static_assert(AUX == 0 || AUX == 2, "plain or non-temporal");
-    if constexpr (AUX == 2)
-        asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen nt lds"
-                     :: "s"(lds_m0(dst)), "v"(voffset), "s"(rs) : "memory");
-    else
-        asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-                     :: "s"(lds_m0(dst)), "v"(voffset), "s"(rs) : "memory");
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)dst, 16, voffset, 0, 0,
+                                             AUX);
 }
 template <int AUX>
 __device__ __forceinline__ void lds_load16(const void* src, u32x4* dst) {
-    static_assert(AUX == 0 || AUX == 2, "plain or non-temporal");
-    if constexpr (AUX == 2)
-        asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off nt" :: "s"(lds_m0(dst)), "v"(src) : "memory");
-    else
-        asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" :: "s"(lds_m0(dst)), "v"(src) : "memory");
+    __builtin_amdgcn_global_load_lds((__attribute__((address_space(1))) void*)const_cast<void*>(src),
+                                     (__attribute__((address_space(3))) void*)dst, 16, 0, AUX);
 }
 // s_waitcnt immediates (gfx9 encoding: vmcnt [3:0] and [15:14], expcnt [6:4],
 // lgkmcnt [11:8]): wait for every vector memory operation (LDS-destination
-// loads included), or for every LDS / scalar memory operation, or for both.
+// loads included), or for every LDS / scalar memory operation.
 constexpr int kWaitVm0   = 0x0F70;
 constexpr int kWaitLgkm0 = 0xC07F;
-constexpr int kWaitAll0  = 0x0070;
-// Wait until at most n vector memory operations are outstanding (n < 64).
-// Vector memory operations complete in issue order, so every operation
-// issued before the last n has then completed.
-constexpr int wait_vm(int n) { return (n & 15) | ((n >> 4) << 14) | 0x0F70; }
 
 // How a step finds its pages.
 enum PagePath : int {
@@ -286,10 +254,8 @@ __device__ __forceinline__ void store_row(float* row, const f32x4 (&oacc)[8], in
 
 // Block-level merge after the split loop. slot_item holds, per wave, the
 // (row, kv head) item of its first (slot 0) and last (slot 1) segment when that
-// segment is a split one, else -1; lse holds the slots' base-2 LSEs and part
-// their normalized partial rows (G x head_dim floats; wave w's slot sl at
-// part + w * wstride + sl * G * head_dim), written to LDS by the wave that
-// computed them.
+// segment is a split one, else -1; part / lse hold the slot's normalized
+// partial rows and base-2 LSEs, written to LDS by the wave that computed them.
 // Items appear in block order (wave, slot) as contiguous runs (ignoring empty
 // slots), and the planner turns this merge on only when every split row lies in
 // one block, so each run is a whole row. Each thread owns one head-dim element
@@ -297,8 +263,8 @@ __device__ __forceinline__ void store_row(float* row, const f32x4 (&oacc)[8], in
 // (no LDS round trip per slot) and forms, per run, the base-2 LSE-weighted
 // average of the run's partials (decode_kernels.cuh:409-432), written as fp16.
 template <int G>
-__device__ __forceinline__ void block_merge(const pa_decode_params& p, const int (*slot_item)[2], const float* part,
-                                            int wstride, const float (*lse)[G], int tid) {
+__device__ __forceinline__ void block_merge(const pa_decode_params& p, const int (*slot_item)[2],
+                                            const float (*part)[G * kHeadDim], const float (*lse)[G], int tid) {
     constexpr int NS = 2 * kWaves;
     constexpr int NO = G * kHeadDim;
     static_assert(NS <= 64, "one lane per slot");
@@ -319,7 +285,7 @@ __device__ __forceinline__ void block_merge(const pa_decode_params& p, const int
 #pragma unroll
         for (int j = 0; j < NS; ++j) {
             lv[j] = lse[j][g];
-            pv[j] = part[(j >> 1) * wstride + (j & 1) * NO + o];
+            pv[j] = part[j][o];
         }
         for (unsigned rs = starts; rs != 0; rs &= rs - 1) {
             const int x = __builtin_amdgcn_readlane(mine, __builtin_ctz(rs));   // the run's item
@@ -370,40 +336,20 @@ __device__ __forceinline__ void decode_split_body(const pa_decode_params& p, int
     constexpr int  CPR   = ROW / 16;                // 16-byte chunks per row
     constexpr int  HCH   = 16 * CPR;                // 16-byte chunks per half (256 B per row x 16)
     constexpr bool DMA   = STG && kLdsDma;          // the stage is filled by LDS-destination loads
-    static_assert(!DMA || DEPTH <= 2, "the LDS-destination stage holds one or two steps");
-    static_assert(!DMA || DEPTH == 1 || G <= 4, "two stage slots fit LDS for up to four query heads per kv head");
-    constexpr int  SD    = DMA ? DEPTH : 1;         // stage slots per wave (one per step in flight)
-    constexpr int  SSTEP = 2 * NH * HCH;            // 16-byte chunks of one step (K and V)
-    // Vector memory operations of one issue() on the LDS-destination paths:
-    // the compact Q loads and the K / V loads, all issued whether or not the
-    // step exists (past a unit's end with an empty range or a repeated row).
-    constexpr int  VM_ISSUE = NQ + 2 * NH * NPART;
-    // With two stage slots the partials of the block-level merge live in the
-    // wave's own stage once its loop is done (a split first segment that ends
-    // earlier is held in registers until then); with one they have LDS of
-    // their own.
-    constexpr bool PALIAS = SD > 1;
-    static_assert(!PALIAS || 2 * G * kHeadDim * 4 <= SSTEP * 16, "partials fit the wave's stage slot 0");
+    static_assert(!DMA || DEPTH == 1, "the LDS-destination stage holds one step");
     using VRaw = std::conditional_t<EB == 2, u32x4, u32x2>;
     using KRaw = std::conditional_t<KL == 16, u32x4, u32x2>;
 
-    // Compact Q per wave (G heads x 256 B). On the LDS-destination paths each
-    // stage slot has its own, filled by the slot's issue() with the K / V.
-    constexpr int QS = DMA ? SD : 1;
-    __shared__ __attribute__((aligned(16))) u32x4 q_lds[kWaves][QS][64 * NQ];
+    // Compact Q per wave (G heads x 256 B; on the LDS-destination paths filled
+    // by issue() with the K / V, 1 KiB per load).
+    __shared__ __attribute__((aligned(16))) u32x4 q_lds[kWaves][64 * NQ];
     __shared__ int slot_item[kWaves][2];                                     // split segments per wave
-    // LDS stage of SD steps per wave (STG): per step [K, V][half][16 rows][row
-    // bytes], each row's 16-byte chunks XOR-swizzled by (row % chunks per row).
-    // Slot 1 is an array of its own, so that the compiler can tell a read of
-    // one slot from the loads landing in the other.
-    __shared__ __attribute__((aligned(16))) u32x4 stage_lds[STG ? kWaves : 1][STG ? SSTEP : 1];
-    __shared__ __attribute__((aligned(16))) u32x4 stage1_lds[SD > 1 ? kWaves : 1][SD > 1 ? SSTEP : 1];
+    // LDS stage of one step per wave (STG): [K, V][half][16 rows][row bytes],
+    // each row's 16-byte chunks XOR-swizzled by (row % chunks per row).
+    __shared__ __attribute__((aligned(16))) u32x4 stage_lds[STG ? kWaves : 1][STG ? 2 * NH * HCH : 1];
     // Partials of split segments for the block-level merge, slot 2 * wave + sl.
-    __shared__ __attribute__((aligned(16))) float part_lds[PALIAS ? 1 : 2 * kWaves][PALIAS ? 1 : G * kHeadDim];
+    __shared__ __attribute__((aligned(16))) float part_lds[2 * kWaves][G * kHeadDim];
     __shared__ float lse_lds[2 * kWaves][G];
-    // Where wave w's merge slot sl lives, and the distance between waves (floats).
-    constexpr int PWSTRIDE = PALIAS ? SSTEP * 4 : 2 * G * kHeadDim;
-    float* const part_base = PALIAS ? reinterpret_cast<float*>(&stage_lds[0][0]) : &part_lds[0][0];
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -441,8 +387,7 @@ __device__ __forceinline__ void decode_split_body(const pa_decode_params& p, int
 #pragma unroll
     for (int part = 0; part < NPART; ++part)
         dma_chunk[part] = 16 * ((lane % CPR) ^ ((RPP * part + lane / CPR) % CPR));
-    u32x4* const stage  = stage_lds[STG ? wave : 0];
-    u32x4* const stage1 = stage1_lds[SD > 1 ? wave : 0];
+    u32x4* const stage = stage_lds[STG ? wave : 0];
 
     // ---- pipeline registers, indexed by ring slot = step index mod DEPTH
     KRaw  kr[DEPTH][NH][NK];   // K: token 16hh + c of each half
@@ -542,9 +487,8 @@ __device__ __forceinline__ void decode_split_body(const pa_decode_params& p, int
 
     // K/V loads of step L into slot s (and Q at a segment start), then advance L.
     auto issue = [&](int s) {
-        u32x4* const sst = SD > 1 && s ? stage1 : stage;   // the slot's stage
         if constexpr (DMA) {
-            // The slot's previous stage and Q reads have returned before new
+            // The previous step's stage and Q reads have returned before new
             // rows land.
             __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
             wave_lds_sync();
@@ -553,15 +497,16 @@ __device__ __forceinline__ void decode_split_body(const pa_decode_params& p, int
         const __amdgpu_buffer_rsrc_t qrs =
             buffer_rsrc(p.q + (static_cast<size_t>(L.b) * hq + L.h * G) * kHeadDim, first ? 256 * G : 0);
         if constexpr (DMA) {
-            // Q lands in the slot's Q area first, so it has arrived once the
-            // step's K / V have (lanes past G x 256 B and steps that start no
-            // segment write zeros).
+            // A segment's Q lands in the wave's Q area with its first K / V
+            // (lanes past G x 256 B write zeros).
+            if (first) {
 #pragma unroll
-            for (int n = 0; n < NQ; ++n) lds_load16<0>(qrs, &q_lds[wave][SD > 1 ? s : 0][64 * n], 16 * (64 * n + lane));
+                for (int n = 0; n < NQ; ++n) lds_load16<0>(qrs, &q_lds[wave][64 * n], 16 * (64 * n + lane));
+            }
         } else {
 #pragma unroll
             for (int n = 0; n < NQ; ++n)
-                qc[DMA ? 0 : s][n] = __builtin_bit_cast(
+                qc[s][n] = __builtin_bit_cast(
                     u32x4, __builtin_amdgcn_raw_buffer_load_b128(qrs, 16 * ((64 * n + lane) % (16 * G)), 0, 0));
         }
         if constexpr (PATH == kPagePow2) {
@@ -581,8 +526,8 @@ __device__ __forceinline__ void decode_split_body(const pa_decode_params& p, int
 #pragma unroll
                     for (int part = 0; part < NPART; ++part) {
                         const int off = 1024 * part + ROW * (lane / CPR) + dma_chunk[part];
-                        lds_load16<kAux<NT>>(krs, sst + hh * HCH + 64 * part, off);
-                        lds_load16<kAux<NT>>(vrs, sst + (NH + hh) * HCH + 64 * part, off);
+                        lds_load16<kAux<NT>>(krs, stage + hh * HCH + 64 * part, off);
+                        lds_load16<kAux<NT>>(vrs, stage + (NH + hh) * HCH + 64 * part, off);
                     }
                     continue;
                 } else if constexpr (STG) {
@@ -629,8 +574,8 @@ __device__ __forceinline__ void decode_split_body(const pa_decode_params& p, int
                     const __amdgpu_buffer_rsrc_t vrs = buffer_rsrc(vbase + row0, nv * ROW);
                     if constexpr (DMA) {
                         const int off = ROW * (lane / CPR) + dma_chunk[part];
-                        lds_load16<kAux<NT>>(krs, sst + hh * HCH + 64 * part, off);
-                        lds_load16<kAux<NT>>(vrs, sst + (NH + hh) * HCH + 64 * part, off);
+                        lds_load16<kAux<NT>>(krs, stage + hh * HCH + 64 * part, off);
+                        lds_load16<kAux<NT>>(vrs, stage + (NH + hh) * HCH + 64 * part, off);
                     } else {
                         kc[s][hh][part] = __builtin_bit_cast(
                             u32x4, __builtin_amdgcn_raw_buffer_load_b128(krs, 16 * lane, 0, kAux<NT>));
@@ -644,14 +589,10 @@ __device__ __forceinline__ void decode_split_body(const pa_decode_params& p, int
 #pragma unroll
                 for (int part = 0; part < NPART; ++part) {
                     const int pgl = __builtin_amdgcn_ds_bpermute(plk[s][hh][part], pent[s]);
-                    size_t row = kv_row_offset<EB>(pgl, L.h, psl[s][hh][part], P, hkv);
+                    const size_t row = kv_row_offset<EB>(pgl, L.h, psl[s][hh][part], P, hkv);
                     if constexpr (DMA) {
-                        // Past the unit's end (two steps in flight issue one
-                        // such step) every lane reads the pools' first row:
-                        // one line instead of the last step again.
-                        if (SD > 1 && !l_more) row = 0;
-                        lds_load16<kAux<NT>>(kbase + row + dma_chunk[part], sst + hh * HCH + 64 * part);
-                        lds_load16<kAux<NT>>(vbase + row + dma_chunk[part], sst + (NH + hh) * HCH + 64 * part);
+                        lds_load16<kAux<NT>>(kbase + row + dma_chunk[part], stage + hh * HCH + 64 * part);
+                        lds_load16<kAux<NT>>(vbase + row + dma_chunk[part], stage + (NH + hh) * HCH + 64 * part);
                     } else {
                         kc[s][hh][part] = load16<NT>(kbase + row + 16 * (lane % CPR));
                         vc[s][hh][part] = load16<NT>(vbase + row + 16 * (lane % CPR));
@@ -693,26 +634,8 @@ __device__ __forceinline__ void decode_split_body(const pa_decode_params& p, int
 #pragma unroll
     for (int j = 0; j < 8; ++j) oacc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    // Two stage slots: a split first segment that ends before the unit's last
-    // step keeps its normalized rows and LSEs here until the loop is done.
-    f32x4 hold[PALIAS ? HW : 1][2];
-    float hold_ls[PALIAS ? HW : 1];
-    bool  held = false;
-
     auto finish_segment = [&]() {
-        const bool last_seg = C.seg + 1 >= seg_end;       // the unit's last segment ends here
-        const int  sl       = C.seg == seg_begin ? 0 : 1;   // a unit's split segments are its first and last
-        if (PALIAS && merge_here && !whole) {
-            if (last_seg) {
-                // The partial goes into the wave's stage: the step past the
-                // unit's end (still loading zeros) and this step's stage reads
-                // complete first.
-                __builtin_amdgcn_s_waitcnt(kWaitAll0);
-                wave_lds_sync();
-            } else {
-                held = true;
-            }
-        }
+        const int sl = C.seg == seg_begin ? 0 : 1;   // a unit's split segments are its first and last
         float lsum = l_run;
         lsum += __shfl_xor(lsum, 16);
         lsum += __shfl_xor(lsum, 32);
@@ -746,20 +669,9 @@ __device__ __forceinline__ void decode_split_body(const pa_decode_params& p, int
                     // The LDS and HBM stores stay in separate branches: a pointer
                     // selected between them would be a generic (flat) address.
                     if (merge_here) {
-                        if (PALIAS && !last_seg) {
-                            // A split first segment that ends before the
-                            // unit's loop: held until the stage is free.
-#pragma unroll
-                            for (int j = 0; j < 4; ++j) {
-                                hold[i][0][j] = oacc[j][i] * inv;
-                                hold[i][1][j] = oacc[4 + j][i] * inv;
-                            }
-                            hold_ls[i] = ls;
-                        } else {
-                            float* lrow = part_base + wave * PWSTRIDE + (sl * G + 4 * kb + i) * kHeadDim;
-                            store_row(lrow, oacc, i, inv, c);
-                            if (c == 0) lse_lds[2 * wave + sl][4 * kb + i] = ls;
-                        }
+                        float* lrow = &part_lds[2 * wave + sl][(4 * kb + i) * kHeadDim];
+                        store_row(lrow, oacc, i, inv, c);
+                        if (c == 0) lse_lds[2 * wave + sl][4 * kb + i] = ls;
                     } else {
                         float* prow = p.partial_out + (static_cast<size_t>(C.seg) * G + 4 * kb + i) * kHeadDim;
                         store_row(prow, oacc, i, inv, c);
@@ -795,17 +707,15 @@ __device__ __forceinline__ void decode_split_body(const pa_decode_params& p, int
 
     auto consume = [&](int s) {
         if constexpr (DMA) {
-            // The step's Q and rows are in its slot once its loads have
-            // returned. With one step in flight every outstanding vector
-            // memory operation is this step's; with two, the other slot's
-            // issue() (VM_ISSUE operations) came after this step's loads and
-            // may stay outstanding.
-            __builtin_amdgcn_s_waitcnt(SD > 1 ? wait_vm(VM_ISSUE) : kWaitVm0);
+            // With one step in flight, every vector memory operation
+            // outstanding here belongs to this step: its Q and rows are in
+            // LDS once they have all returned.
+            __builtin_amdgcn_s_waitcnt(kWaitVm0);
             wave_lds_sync();
         }
         if (__builtin_expect(C.tok == C.t0, 0)) {
             // Q of the new segment: compact -> LDS -> B-operand layout.
-            u32x4* ql = q_lds[wave][SD > 1 ? s : 0];
+            u32x4* ql = q_lds[wave];
             if constexpr (!DMA) {
                 wave_lds_sync();   // the previous segment's Q reads are done
 #pragma unroll
@@ -822,7 +732,7 @@ __device__ __forceinline__ void decode_split_body(const pa_decode_params& p, int
         if constexpr (STG) {
             // Coalesced rows -> LDS (16-byte chunk j of row r at chunk j ^ (r % CPR))
             // -> the K / V lane layouts of the direct loads.
-            u32x4* st = SD > 1 && s ? stage1 : stage;
+            u32x4* st = stage;
             if constexpr (!DMA) {
                 const int wrow = lane / CPR;   // row within a 1 KiB part
                 wave_lds_sync();   // the previous step's stage reads are done
@@ -1005,28 +915,11 @@ __device__ __forceinline__ void decode_split_body(const pa_decode_params& p, int
         if constexpr (DEPTH > 2) if (!advance(2)) break;
         if constexpr (DEPTH > 3) if (!advance(3)) break;
     }
-    if constexpr (DMA) {
-        // No LDS-destination load is left in flight when the wave ends; with
-        // two stage slots the held first-segment partial now has its place.
-        __builtin_amdgcn_s_waitcnt(kWaitAll0);
-        wave_lds_sync();
-    }
-    if constexpr (PALIAS) {
-        if (held && 4 * kb < G) {
-#pragma unroll
-            for (int i = 0; i < HW; ++i) {
-                float* lrow = part_base + wave * PWSTRIDE + (4 * kb + i) * kHeadDim;   // slot 0
-                *reinterpret_cast<f32x4*>(lrow + 8 * c)     = hold[i][0];
-                *reinterpret_cast<f32x4*>(lrow + 8 * c + 4) = hold[i][1];
-                if (c == 0) lse_lds[2 * wave][4 * kb + i] = hold_ls[i];
-            }
-        }
-    }
     }   // seg_begin < seg_end
 
     if (merge_here) {
         __syncthreads();
-        block_merge<G>(p, slot_item, part_base, PWSTRIDE, lse_lds, threadIdx.x);
+        block_merge<G>(p, slot_item, part_lds, lse_lds, threadIdx.x);
     }
 }
 
@@ -1159,16 +1052,11 @@ __global__ __launch_bounds__(64 * WAVES) void decode_merge_kernel(const pa_decod
 #ifndef PA_FP8_LANE_DEPTH
 #define PA_FP8_LANE_DEPTH 2
 #endif
-// Through LDS-destination loads the per-lane path keeps one step: its
-// per-lane page-table read is a vector load the compiler waits for with
-// vmcnt(0), which would drain a second slot every step.
 template <int EB> constexpr int kLaneDepth = kLdsDma ? 1 : EB == 2 ? PA_FP16_LANE_DEPTH : PA_FP8_LANE_DEPTH;
-// Steps in flight on the power-of-two path and on the staged small-page path:
-// through LDS-destination loads, kDmaDepth for up to four query heads per kv
-// head (two slots with their Q areas do not fit LDS at eight).
-template <int G> constexpr int kDmaDepthG = G <= 4 ? kDmaDepth : 1;
-template <int EB, int G> constexpr int kPow2Depth = kLdsDma && Tune<EB>::stage ? kDmaDepthG<G> : Tune<EB>::depth;
-template <int EB, int G> constexpr int kRunsDepth = kLdsDma ? kDmaDepthG<G> : Tune<EB>::depth;
+// Steps in flight on the power-of-two path (one when it is staged through
+// LDS-destination loads) and on the staged small-page path.
+template <int EB> constexpr int kPow2Depth = kLdsDma && Tune<EB>::stage ? 1 : Tune<EB>::depth;
+template <int EB> constexpr int kRunsDepth = kLdsDma ? 1 : Tune<EB>::depth;
 
 template <int EB, int G, int NG, int DEPTH, int PATH>
 hipError_t launch_split_p(const pa_decode_params& p, int shift, hipStream_t s) {
@@ -1191,14 +1079,14 @@ hipError_t launch_split_g(const pa_decode_params& p, hipStream_t s) {
         // Byte offsets of one page and of one (kv head, slot) inside it are 32-bit.
         if (static_cast<long long>(p.num_kv_heads) * P * kRowBytes<EB> >= (1ll << 31))
             throw std::invalid_argument("decode: page_size * num_kv_heads * row bytes must be below 2^31");
-        return launch_split_p<EB, G, Tune<EB>::step, kPow2Depth<EB, G>, kPagePow2>(p, shift, s);
+        return launch_split_p<EB, G, Tune<EB>::step, kPow2Depth<EB>, kPagePow2>(p, shift, s);
     }
     if constexpr (EB == 2 || Tune<EB>::stage) {
         // Pages of whole 1 KiB parts (4 fp16 rows, 8 FP8 rows) through the LDS stage.
         if (P == 8 || (EB == 2 && P == 4)) {
             if (static_cast<long long>(p.num_kv_heads) * P * kRowBytes<EB> >= (1ll << 31))
                 throw std::invalid_argument("decode: page_size * num_kv_heads * row bytes must be below 2^31");
-            return launch_split_p<EB, G, Tune<EB>::step, kRunsDepth<EB, G>, kPageRuns>(p, shift, s);
+            return launch_split_p<EB, G, Tune<EB>::step, kRunsDepth<EB>, kPageRuns>(p, shift, s);
         }
         // Any other size: per-lane rows through the LDS stage (shift -1: divide).
         return launch_split_p<EB, G, Tune<EB>::step, kLaneDepth<EB>, kPageLane>(p, pow2 ? shift : -1, s);
@@ -1259,10 +1147,10 @@ template <int EB, int G>
 const void* split_symbol() {
     if constexpr (EB == 2)
         return reinterpret_cast<const void*>(
-            &decode_split_kernel_f16<G, Tune<EB>::step, kPow2Depth<EB, G>, kPagePow2>);
+            &decode_split_kernel_f16<G, Tune<EB>::step, kPow2Depth<EB>, kPagePow2>);
     else
         return reinterpret_cast<const void*>(
-            &decode_split_kernel_fp8<G, Tune<EB>::step, kPow2Depth<EB, G>, kPagePow2>);
+            &decode_split_kernel_fp8<G, Tune<EB>::step, kPow2Depth<EB>, kPagePow2>);
 }
 
 }  // namespace
