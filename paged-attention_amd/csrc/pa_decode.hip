@@ -252,52 +252,73 @@ __device__ __forceinline__ void store_row(float* row, const f32x4 (&oacc)[8], in
     *reinterpret_cast<f32x4*>(row + 8 * c + 4) = hi;
 }
 
+// x from the lane that DPP control CTRL selects within each row of 16 lanes.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float x) {
+    const int v = __builtin_bit_cast(int, x);
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(v, v, CTRL, 0xF, 0xF, false));
+}
+
 // Block-level merge after the split loop. slot_item holds, per wave, the
 // (row, kv head) item of its first (slot 0) and last (slot 1) segment when that
 // segment is a split one, else -1; part / lse hold the slot's normalized
 // partial rows and base-2 LSEs, written to LDS by the wave that computed them.
-// Items appear in block order (wave, slot) as contiguous runs (ignoring empty
-// slots), and the planner turns this merge on only when every split row lies in
-// one block, so each run is a whole row. Each thread owns one head-dim element
-// (two for G = 8) of every run: it reads that element of all 16 slots at once
-// (no LDS round trip per slot) and forms, per run, the base-2 LSE-weighted
-// average of the run's partials (decode_kernels.cuh:409-432), written as fp16.
+// The planner turns this merge on only when every split row lies in one block,
+// so the slots holding one item are that row's whole set of partials. Each
+// thread owns one head-dim element (two for G = 8) of every item and reads
+// that element of all 16 slots at once, with the LSEs and slot items (one LDS
+// round trip). An item's weights 2^(lse - max) depend only on the slot and the
+// head, and a wave's 64 elements share one head, so lane j of each wave
+// computes slot j's weight once (0 outside the item) and the element sums take
+// them as wave-uniform operands: per item, the base-2 LSE-weighted average of
+// its partials (decode_kernels.cuh:409-432), summed in slot order, written as
+// fp16. No branch depends on a slot.
 template <int G>
 __device__ __forceinline__ void block_merge(const pa_decode_params& p, const int (*slot_item)[2],
                                             const float (*part)[G * kHeadDim], const float (*lse)[G], int tid) {
     constexpr int NS = 2 * kWaves;
     constexpr int NO = G * kHeadDim;
-    static_assert(NS <= 64, "one lane per slot");
-    const int mine = slot_item[(tid & (NS - 1)) >> 1][tid & 1];
-    int item[NS];
-    unsigned starts = 0;   // slots that begin a run
-    int prev = -1;
+    constexpr int NE = (NO + 64 * kWaves - 1) / (64 * kWaves);   // elements per thread
+    static_assert(NS == 16, "the slot lanes form one DPP row");
+    static_assert(kHeadDim % 64 == 0, "a wave's elements share one head");
+    const int  lane = tid & 63;
+    const bool slot = lane < NS;   // lane j holds slot j
+    float lv[NE], pv[NE][NS];
 #pragma unroll
-    for (int s = 0; s < NS; ++s) {
-        item[s] = __builtin_amdgcn_readlane(mine, s);
-        if (item[s] >= 0 && item[s] != prev) starts |= 1u << s;
-        if (item[s] >= 0) prev = item[s];
-    }
+    for (int e = 0; e < NE; ++e) {
+        const int o = tid + 64 * kWaves * e;
+        if (o < NO) {
+            lv[e] = lse[lane & (NS - 1)][o / kHeadDim];
 #pragma unroll
-    for (int o = tid; o < NO; o += 64 * kWaves) {
-        const int g = o / kHeadDim;
-        float lv[NS], pv[NS];
-#pragma unroll
-        for (int j = 0; j < NS; ++j) {
-            lv[j] = lse[j][g];
-            pv[j] = part[j][o];
+            for (int j = 0; j < NS; ++j) pv[e][j] = part[j][o];
         }
-        for (unsigned rs = starts; rs != 0; rs &= rs - 1) {
-            const int x = __builtin_amdgcn_readlane(mine, __builtin_ctz(rs));   // the run's item
-            float mx = -INFINITY;
+    }
+    const int      mine   = slot_item[(lane & (NS - 1)) >> 1][lane & 1];
+    const uint64_t filled = __builtin_amdgcn_ballot_w64(slot && mine >= 0);
 #pragma unroll
-            for (int j = 0; j < NS; ++j) mx = item[j] == x ? fmaxf(mx, lv[j]) : mx;
+    for (int e = 0; e < NE; ++e) {
+        const int o = tid + 64 * kWaves * e;
+        if (o >= NO) break;
+        uint64_t run = 0;
+        for (uint64_t rem = filled; rem != 0; rem &= ~run) {
+            const int x = __builtin_amdgcn_readlane(mine, __builtin_ctzll(rem));   // the next item
+            run = __builtin_amdgcn_ballot_w64(slot && mine == x);
+            const bool in = (run >> lane) & 1;
+            // The item's maximum LSE over the 16 slot lanes (one DPP row):
+            // swaps of neighbours and pairs in each quad, then rotations by 4
+            // and 8.
+            float mx = in ? lv[e] : -INFINITY;
+            mx = fmaxf(mx, dpp_f32<0xB1>(mx));    // quad_perm [1,0,3,2]
+            mx = fmaxf(mx, dpp_f32<0x4E>(mx));    // quad_perm [2,3,0,1]
+            mx = fmaxf(mx, dpp_f32<0x124>(mx));   // row_ror:4
+            mx = fmaxf(mx, dpp_f32<0x128>(mx));   // row_ror:8
+            const float w = in ? exp2_fast(lv[e] - mx) : 0.f;
             float a = 0.f, den = 0.f;
 #pragma unroll
             for (int j = 0; j < NS; ++j) {
-                const float w = exp2_fast(lv[j] - mx);
-                a   = item[j] == x ? fmaf(w, pv[j], a) : a;
-                den = item[j] == x ? den + w : den;
+                const float wj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), j));
+                a   = fmaf(wj, ((run >> j) & 1) ? pv[e][j] : 0.f, a);   // empty slots hold no partial
+                den = den + wj;
             }
             const int b = x / p.num_kv_heads, h = x - b * p.num_kv_heads;
             p.out[(static_cast<size_t>(b) * p.num_q_heads + h * G) * kHeadDim + o] =
