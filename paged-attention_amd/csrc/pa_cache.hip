@@ -95,74 +95,87 @@ __device__ __forceinline__ u32x2 encode8_hw(const u32x4 in, float inv) {
     return out;
 }
 
-// Stores one 8-dim chunk of fp16 K and V at byte offset dst of the pools:
-// a bit copy (fp16) or e4m3(float(x) * inv_scale) (FP8, paged_kv_cache.cu:15-22).
+// E4M3 bytes of eight products float(x) * inv, in software (e4m3_encode).
+__device__ __forceinline__ u32x2 encode8_sw(const u32x4 in, float inv) {
+    u32x2 out = {0u, 0u};
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+        out[e >> 2] |= e4m3_encode(f16_bits_to_f32((in[e >> 1] >> (16 * (e & 1))) & 0xffffu) * inv) << (8 * (e & 3));
+    return out;
+}
+
+__device__ __forceinline__ u32x2 encode8(const u32x4 in, float inv) {
+    if constexpr (kAppendHwCvt) return encode8_hw(in, inv);
+    else return encode8_sw(in, inv);
+}
+
+// Dims of one row that one thread appends: 8 for fp16 (one 16-byte load and
+// one 16-byte store per pool), 16 for FP8 (two 16-byte loads of fp16, one
+// 16-byte store of E4M3 bytes).
 template <int EB>
-__device__ __forceinline__ void store_chunk(const u32x4 kin, const u32x4 vin, void* k_cache, void* v_cache, size_t dst,
-                                            float inv_k, float inv_v) {
+constexpr int kAppendDims = EB == 2 ? 8 : 16;
+
+template <bool NT, typename T>
+__device__ __forceinline__ void store_raw(T x, unsigned char* p) {
+    if constexpr (NT) __builtin_nontemporal_store(x, reinterpret_cast<T*>(p));
+    else *reinterpret_cast<T*>(p) = x;
+}
+
+// Appends one kAppendDims-dim chunk of K and V: fp16 elements from element
+// offset src of k / v to byte offset dst of the pools, as a bit copy (fp16) or
+// e4m3(float(x) * inv_scale) (FP8, paged_kv_cache.cu:15-22).
+template <int EB>
+__device__ __forceinline__ void append_chunk(const uint16_t* k, const uint16_t* v, size_t src, void* k_cache,
+                                             void* v_cache, size_t dst, float inv_k, float inv_v) {
     unsigned char* kc = static_cast<unsigned char*>(k_cache) + dst;
     unsigned char* vc = static_cast<unsigned char*>(v_cache) + dst;
+    // Every load is issued before the first store: a store may alias the
+    // inputs as far as the compiler knows, so a load after it would wait.
     if constexpr (EB == 2) {
-        if constexpr (kAppendNT) {
-            __builtin_nontemporal_store(kin, reinterpret_cast<u32x4*>(kc));
-            __builtin_nontemporal_store(vin, reinterpret_cast<u32x4*>(vc));
-        } else {
-            *reinterpret_cast<u32x4*>(kc) = kin;
-            *reinterpret_cast<u32x4*>(vc) = vin;
-        }
+        const u32x4 k0 = load16<kAppendNT>(k + src), v0 = load16<kAppendNT>(v + src);
+        store_raw<kAppendNT>(k0, kc);
+        store_raw<kAppendNT>(v0, vc);
     } else {
-        u32x2 ko = {0u, 0u}, vo = {0u, 0u};
-        if constexpr (kAppendHwCvt) {
-            ko = encode8_hw(kin, inv_k);
-            vo = encode8_hw(vin, inv_v);
-        } else {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const uint32_t kh = (kin[e >> 1] >> (16 * (e & 1))) & 0xffffu;
-                const uint32_t vh = (vin[e >> 1] >> (16 * (e & 1))) & 0xffffu;
-                ko[e >> 2] |= e4m3_encode(f16_bits_to_f32(kh) * inv_k) << (8 * (e & 3));
-                vo[e >> 2] |= e4m3_encode(f16_bits_to_f32(vh) * inv_v) << (8 * (e & 3));
-            }
-        }
-        if constexpr (kAppendNT) {
-            __builtin_nontemporal_store(ko, reinterpret_cast<u32x2*>(kc));
-            __builtin_nontemporal_store(vo, reinterpret_cast<u32x2*>(vc));
-        } else {
-            *reinterpret_cast<u32x2*>(kc) = ko;
-            *reinterpret_cast<u32x2*>(vc) = vo;
-        }
+        const u32x4 k0 = load16<kAppendNT>(k + src), k1 = load16<kAppendNT>(k + src + 8);
+        const u32x4 v0 = load16<kAppendNT>(v + src), v1 = load16<kAppendNT>(v + src + 8);
+        const u32x2 ka = encode8(k0, inv_k), kb = encode8(k1, inv_k);
+        const u32x2 va = encode8(v0, inv_v), vb = encode8(v1, inv_v);
+        store_raw<kAppendNT>(u32x4{ka[0], ka[1], kb[0], kb[1]}, kc);
+        store_raw<kAppendNT>(u32x4{va[0], va[1], vb[0], vb[1]}, vc);
     }
 }
 
-// One thread per (token, kv head, 8-dim chunk); token i goes to position
-// start_pos + i of the sequence whose block-table row is bt_row.
+// One thread per (token, kv head, chunk of kAppendDims dims); token i goes to
+// position start_pos + i of the sequence whose block-table row is bt_row.
 template <int EB>
 __global__ __launch_bounds__(256) void append_kernel(const uint16_t* __restrict__ k,
                                                      const uint16_t* __restrict__ v, void* k_cache,
                                                      void* v_cache, const int32_t* __restrict__ bt_row,
                                                      int start_pos, int n, int hkv, int page_size,
                                                      float inv_k, float inv_v) {
+    constexpr int DIMS = kAppendDims<EB>, CPR = kHeadDim / DIMS;
     const int idx = blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= n * hkv * (kHeadDim / 8)) return;
-    const int chunk = idx & 15;
-    const int th    = idx >> 4;
+    if (idx >= n * hkv * CPR) return;
+    const int chunk = static_cast<unsigned>(idx) % CPR;   // idx >= 0: a mask and a shift
+    const int th    = static_cast<unsigned>(idx) / CPR;
     const int h     = th % hkv;
     const int i     = th / hkv;
     const int pos   = start_pos + i;
     const int page  = bt_row[pos / page_size];
-    const size_t dst = kv_row_offset<EB>(page, h, pos % page_size, page_size, hkv) + 8 * EB * chunk;
-    const size_t src = (static_cast<size_t>(i) * hkv + h) * kHeadDim + 8 * chunk;
-    store_chunk<EB>(load16<kAppendNT>(k + src), load16<kAppendNT>(v + src), k_cache, v_cache, dst, inv_k, inv_v);
+    const size_t dst = kv_row_offset<EB>(page, h, pos % page_size, page_size, hkv) + DIMS * EB * chunk;
+    const size_t src = (static_cast<size_t>(i) * hkv + h) * kHeadDim + DIMS * chunk;
+    append_chunk<EB>(k, v, src, k_cache, v_cache, dst, inv_k, inv_v);
 }
 
 // A whole batch of appends in one launch (layout of AppendBatch::meta in
-// pa_internal.hpp). Threads cover max(n_tok * hkv * 16, n_tab, n_len); each
-// writes its 8-dim chunk, table entry and length where it has one. A token
+// pa_internal.hpp). Threads cover max(n_tok * hkv * chunks per row, n_tab,
+// n_len); each writes its chunk, table entry and length where it has one. A token
 // finds its entry by binary search over the entries' first-token offsets, then
 // its page in the entry's page list: table entries are read from the staging
 // copy, never from the block table this launch is writing.
 template <int EB>
 __global__ __launch_bounds__(256) void append_batch_kernel(const AppendBatch a) {
+    constexpr int DIMS = kAppendDims<EB>, CPR = kHeadDim / DIMS;
     const int idx = blockIdx.x * blockDim.x + threadIdx.x;
     const int32_t* tok_begin = a.meta;
     const int32_t* old_len   = a.meta + a.n_ent;
@@ -172,9 +185,9 @@ __global__ __launch_bounds__(256) void append_batch_kernel(const AppendBatch a) 
     const int32_t* lens      = tab + 2 * a.n_tab;
     if (idx < a.n_tab) a.table[tab[2 * idx]] = tab[2 * idx + 1];
     if (idx < a.n_len) a.seq_lens[lens[2 * idx]] = lens[2 * idx + 1];
-    if (idx >= a.n_tok * a.hkv * (kHeadDim / 8)) return;
-    const int chunk = idx & 15;
-    const int th    = idx >> 4;
+    if (idx >= a.n_tok * a.hkv * CPR) return;
+    const int chunk = static_cast<unsigned>(idx) % CPR;
+    const int th    = static_cast<unsigned>(idx) / CPR;
     const int h     = th % a.hkv;
     const int t     = th / a.hkv;
     int lo = 0, hi = a.n_ent;   // last entry with tok_begin <= t (zero-count entries share the next one's)
@@ -186,10 +199,9 @@ __global__ __launch_bounds__(256) void append_batch_kernel(const AppendBatch a) 
     const int first = old_len[lo];
     const int pos   = first + (t - tok_begin[lo]);
     const int page  = pages[pl_begin[lo] + pos / a.page_size - first / a.page_size];
-    const size_t dst = kv_row_offset<EB>(page, h, pos % a.page_size, a.page_size, a.hkv) + 8 * EB * chunk;
-    const size_t src = (static_cast<size_t>(t) * a.hkv + h) * kHeadDim + 8 * chunk;
-    store_chunk<EB>(load16<kAppendNT>(a.k + src), load16<kAppendNT>(a.v + src), a.k_cache, a.v_cache, dst, a.inv_k,
-                    a.inv_v);
+    const size_t dst = kv_row_offset<EB>(page, h, pos % a.page_size, a.page_size, a.hkv) + DIMS * EB * chunk;
+    const size_t src = (static_cast<size_t>(t) * a.hkv + h) * kHeadDim + DIMS * chunk;
+    append_chunk<EB>(a.k, a.v, src, a.k_cache, a.v_cache, dst, a.inv_k, a.inv_v);
 }
 
 // One thread per (token, 8-dim chunk) of one kv head: raw cache bytes out,
@@ -287,7 +299,7 @@ hipError_t launch_append(int dtype, const uint16_t* k, const uint16_t* v, void* 
                          float inv_v, hipStream_t s) {
     check_kv_dtype(dtype);
     if (n <= 0) return hipSuccess;
-    const long threads = static_cast<long>(n) * hkv * (kHeadDim / 8);
+    const long threads = static_cast<long>(n) * hkv * (kHeadDim / (dtype == PA_KV_FP16 ? kAppendDims<2> : kAppendDims<1>));
     const int blocks   = static_cast<int>((threads + 255) / 256);
     if (dtype == PA_KV_FP16)
         hipLaunchKernelGGL(append_kernel<2>, dim3(blocks), dim3(256), 0, s, k, v, k_cache, v_cache, bt_row,
@@ -300,7 +312,8 @@ hipError_t launch_append(int dtype, const uint16_t* k, const uint16_t* v, void* 
 
 hipError_t launch_append_batch(int dtype, const AppendBatch& a, hipStream_t s) {
     check_kv_dtype(dtype);
-    const long threads = std::max<long>(static_cast<long>(a.n_tok) * a.hkv * (kHeadDim / 8), std::max(a.n_tab, a.n_len));
+    const int  cpr     = kHeadDim / (dtype == PA_KV_FP16 ? kAppendDims<2> : kAppendDims<1>);
+    const long threads = std::max<long>(static_cast<long>(a.n_tok) * a.hkv * cpr, std::max(a.n_tab, a.n_len));
     if (threads <= 0) return hipSuccess;
     const int blocks = static_cast<int>((threads + 255) / 256);
     if (dtype == PA_KV_FP16)
