@@ -13,6 +13,7 @@
 #include "pa_device.hpp"
 
 #include <algorithm>
+#include <climits>
 #include <cmath>
 #include <cstdint>
 #include <stdexcept>
@@ -121,25 +122,40 @@ __device__ __forceinline__ void store_raw(T x, unsigned char* p) {
     else *reinterpret_cast<T*>(p) = x;
 }
 
-// Appends one kAppendDims-dim chunk of K and V: fp16 elements from element
-// offset src of k / v to byte offset dst of the pools, as a bit copy (fp16) or
+// One kAppendDims-dim chunk of fp16 K and V (one or two 16-byte words each).
+template <int EB>
+struct ChunkIn {
+    u32x4 k[EB == 2 ? 1 : 2], v[EB == 2 ? 1 : 2];
+};
+
+// Loads the chunk at element offset src of k / v. The kernels issue these
+// loads before they look up the destination page, so the two overlap, and
+// before any store: a store may alias the inputs as far as the compiler
+// knows, so a load after it would wait for it.
+template <int EB>
+__device__ __forceinline__ ChunkIn<EB> load_chunk(const uint16_t* k, const uint16_t* v, size_t src) {
+    ChunkIn<EB> in;
+#pragma unroll
+    for (int w = 0; w < (EB == 2 ? 1 : 2); ++w) {
+        in.k[w] = load16<kAppendNT>(k + src + 8 * w);
+        in.v[w] = load16<kAppendNT>(v + src + 8 * w);
+    }
+    return in;
+}
+
+// Stores a chunk at byte offset dst of the pools, as a bit copy (fp16) or
 // e4m3(float(x) * inv_scale) (FP8, paged_kv_cache.cu:15-22).
 template <int EB>
-__device__ __forceinline__ void append_chunk(const uint16_t* k, const uint16_t* v, size_t src, void* k_cache,
-                                             void* v_cache, size_t dst, float inv_k, float inv_v) {
+__device__ __forceinline__ void store_chunk(const ChunkIn<EB>& in, void* k_cache, void* v_cache, size_t dst,
+                                            float inv_k, float inv_v) {
     unsigned char* kc = static_cast<unsigned char*>(k_cache) + dst;
     unsigned char* vc = static_cast<unsigned char*>(v_cache) + dst;
-    // Every load is issued before the first store: a store may alias the
-    // inputs as far as the compiler knows, so a load after it would wait.
     if constexpr (EB == 2) {
-        const u32x4 k0 = load16<kAppendNT>(k + src), v0 = load16<kAppendNT>(v + src);
-        store_raw<kAppendNT>(k0, kc);
-        store_raw<kAppendNT>(v0, vc);
+        store_raw<kAppendNT>(in.k[0], kc);
+        store_raw<kAppendNT>(in.v[0], vc);
     } else {
-        const u32x4 k0 = load16<kAppendNT>(k + src), k1 = load16<kAppendNT>(k + src + 8);
-        const u32x4 v0 = load16<kAppendNT>(v + src), v1 = load16<kAppendNT>(v + src + 8);
-        const u32x2 ka = encode8(k0, inv_k), kb = encode8(k1, inv_k);
-        const u32x2 va = encode8(v0, inv_v), vb = encode8(v1, inv_v);
+        const u32x2 ka = encode8(in.k[0], inv_k), kb = encode8(in.k[1], inv_k);
+        const u32x2 va = encode8(in.v[0], inv_v), vb = encode8(in.v[1], inv_v);
         store_raw<kAppendNT>(u32x4{ka[0], ka[1], kb[0], kb[1]}, kc);
         store_raw<kAppendNT>(u32x4{va[0], va[1], vb[0], vb[1]}, vc);
     }
@@ -160,11 +176,49 @@ __global__ __launch_bounds__(256) void append_kernel(const uint16_t* __restrict_
     const int th    = static_cast<unsigned>(idx) / CPR;
     const int h     = th % hkv;
     const int i     = th / hkv;
+    const ChunkIn<EB> in = load_chunk<EB>(k, v, (static_cast<size_t>(i) * hkv + h) * kHeadDim + DIMS * chunk);
     const int pos   = start_pos + i;
     const int page  = bt_row[pos / page_size];
     const size_t dst = kv_row_offset<EB>(page, h, pos % page_size, page_size, hkv) + DIMS * EB * chunk;
-    const size_t src = (static_cast<size_t>(i) * hkv + h) * kHeadDim + DIMS * chunk;
-    append_chunk<EB>(k, v, src, k_cache, v_cache, dst, inv_k, inv_v);
+    store_chunk<EB>(in, k_cache, v_cache, dst, inv_k, inv_v);
+}
+
+// The chunk of thread idx of append_batch_kernel.
+template <int EB>
+__device__ __forceinline__ void append_batch_chunk(const AppendBatch& a, int idx) {
+    constexpr int DIMS = kAppendDims<EB>, CPR = kHeadDim / DIMS;
+    const int32_t* tok_begin = a.meta;
+    const int32_t* old_len   = a.meta + a.n_ent;
+    const int32_t* pl_begin  = a.meta + 2 * a.n_ent;
+    const int32_t* pages     = a.meta + 3 * a.n_ent;
+    const int chunk = static_cast<unsigned>(idx) % CPR;
+    const int th    = static_cast<unsigned>(idx) / CPR;
+    const int h     = th % a.hkv;
+    const int t     = th / a.hkv;
+    const ChunkIn<EB> in = load_chunk<EB>(a.k, a.v, (static_cast<size_t>(t) * a.hkv + h) * kHeadDim + DIMS * chunk);
+    // The last entry with tok_begin <= t (zero-count entries share the next
+    // one's). Entry t * n_ent / n_tok is tried first (one round of loads): it
+    // is the one when every entry holds the same number of tokens (one in a
+    // decode step, the prompt length in a uniform prefill); otherwise a
+    // binary search.
+    const int g  = min(static_cast<int>(static_cast<int64_t>(t) * a.n_ent / a.n_tok), a.n_ent - 1);
+    const int tg = tok_begin[g];
+    const int tn = g + 1 < a.n_ent ? tok_begin[g + 1] : INT_MAX;
+    int lo = g;
+    if (tg > t || tn <= t) {
+        lo = 0;
+        int hi = a.n_ent;
+        while (hi - lo > 1) {
+            const int mid = (lo + hi) >> 1;
+            if (tok_begin[mid] <= t) lo = mid;
+            else hi = mid;
+        }
+    }
+    const int first = old_len[lo];
+    const int pos   = first + (t - tok_begin[lo]);
+    const int page  = pages[pl_begin[lo] + pos / a.page_size - first / a.page_size];
+    const size_t dst = kv_row_offset<EB>(page, h, pos % a.page_size, a.page_size, a.hkv) + DIMS * EB * chunk;
+    store_chunk<EB>(in, a.k_cache, a.v_cache, dst, a.inv_k, a.inv_v);
 }
 
 // A whole batch of appends in one launch (layout of AppendBatch::meta in
@@ -175,33 +229,22 @@ __global__ __launch_bounds__(256) void append_kernel(const uint16_t* __restrict_
 // copy, never from the block table this launch is writing.
 template <int EB>
 __global__ __launch_bounds__(256) void append_batch_kernel(const AppendBatch a) {
-    constexpr int DIMS = kAppendDims<EB>, CPR = kHeadDim / DIMS;
+    constexpr int CPR = kHeadDim / kAppendDims<EB>;
     const int idx = blockIdx.x * blockDim.x + threadIdx.x;
-    const int32_t* tok_begin = a.meta;
-    const int32_t* old_len   = a.meta + a.n_ent;
-    const int32_t* pl_begin  = a.meta + 2 * a.n_ent;
-    const int32_t* pages     = a.meta + 3 * a.n_ent;
-    const int32_t* tab       = pages + a.n_pl;
+    const int32_t* tab       = a.meta + 3 * a.n_ent + a.n_pl;
     const int32_t* lens      = tab + 2 * a.n_tab;
-    if (idx < a.n_tab) a.table[tab[2 * idx]] = tab[2 * idx + 1];
-    if (idx < a.n_len) a.seq_lens[lens[2 * idx]] = lens[2 * idx + 1];
-    if (idx >= a.n_tok * a.hkv * CPR) return;
-    const int chunk = static_cast<unsigned>(idx) % CPR;
-    const int th    = static_cast<unsigned>(idx) / CPR;
-    const int h     = th % a.hkv;
-    const int t     = th / a.hkv;
-    int lo = 0, hi = a.n_ent;   // last entry with tok_begin <= t (zero-count entries share the next one's)
-    while (hi - lo > 1) {
-        const int mid = (lo + hi) >> 1;
-        if (tok_begin[mid] <= t) lo = mid;
-        else hi = mid;
-    }
-    const int first = old_len[lo];
-    const int pos   = first + (t - tok_begin[lo]);
-    const int page  = pages[pl_begin[lo] + pos / a.page_size - first / a.page_size];
-    const size_t dst = kv_row_offset<EB>(page, h, pos % a.page_size, a.page_size, a.hkv) + DIMS * EB * chunk;
-    const size_t src = (static_cast<size_t>(t) * a.hkv + h) * kHeadDim + DIMS * chunk;
-    append_chunk<EB>(a.k, a.v, src, a.k_cache, a.v_cache, dst, a.inv_k, a.inv_v);
+    // A thread's table entry and length are read first and written last, so
+    // that every load of the thread is issued before its first store. Both
+    // are 8-byte pairs read through buffer resources sized to their arrays:
+    // threads past an array read zeros without a branch (a branch around the
+    // load would make the thread wait for it where the paths join).
+    const u32x2 tabv = __builtin_bit_cast(
+        u32x2, __builtin_amdgcn_raw_buffer_load_b64(buffer_rsrc(tab, 8 * a.n_tab), 8 * min(idx, a.n_tab), 0, 0));
+    const u32x2 lenv = __builtin_bit_cast(
+        u32x2, __builtin_amdgcn_raw_buffer_load_b64(buffer_rsrc(lens, 8 * a.n_len), 8 * min(idx, a.n_len), 0, 0));
+    if (idx < a.n_tok * a.hkv * CPR) append_batch_chunk<EB>(a, idx);
+    if (idx < a.n_tab) a.table[tabv[0]] = static_cast<int32_t>(tabv[1]);
+    if (idx < a.n_len) a.seq_lens[lenv[0]] = static_cast<int32_t>(lenv[1]);
 }
 
 // One thread per (token, 8-dim chunk) of one kv head: raw cache bytes out,

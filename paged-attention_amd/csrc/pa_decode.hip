@@ -132,9 +132,7 @@ namespace {
 constexpr int   kWaves        = kBlockUnits;   // waves (work units) per block
 constexpr float kRescaleSlack = 8.0f;   // log2 headroom of the lazy running max
 constexpr float kLog2e        = 1.4426950408889634f;
-// dword 3 of a raw buffer resource (32-bit data format, no swizzle), and the
-// cache-policy operand of buffer loads (2 = non-temporal).
-constexpr int kBufferFlags = 0x00020000;
+// The cache-policy operand of buffer loads (2 = non-temporal).
 template <bool NT> constexpr int kAux = NT ? 2 : 0;
 
 template <int EB> struct Tune {
@@ -233,10 +231,6 @@ template <int G>
 __device__ __forceinline__ float head_pick(const float (&arr)[G], int kb, int i) {
     if constexpr (G > 4) return kb ? arr[4 + i] : arr[i];
     else return arr[i < G ? i : 0];
-}
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, int bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, kBufferFlags);
 }
 
 // One normalized O row (head row i of the lane's accumulators) of a split

@@ -29,6 +29,15 @@ __device__ __forceinline__ size_t kv_row_offset(int page, int h, int slot, int p
 
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// dword 3 of a raw buffer resource (32-bit data format, no swizzle).
+constexpr int kBufferFlags = 0x00020000;
+
+// Raw buffer resource over [base, base + bytes): loads past the end read
+// zeros and touch no memory.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, int bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, kBufferFlags);
+}
+
 // Orders LDS accesses that lanes of one wave use to trade data: every access
 // before the call (e.g. one lane's ds_write) happens before every access after
 // it (another lane's ds_read of the same bytes). LDS runs a wave's operations
