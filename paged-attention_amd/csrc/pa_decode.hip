@@ -24,7 +24,9 @@
 //     the FP8 kernel instead loads each 16-token half fully coalesced (16 B
 //     per lane, 8 whole rows per instruction) straight into a per-wave LDS
 //     stage (LDS-destination buffer loads, one step in flight) and reads the
-//     layouts from there. The stage's 16-byte chunks are XOR-swizzled by row
+//     layouts from there into registers at the top of each step, after which
+//     the next step's loads are issued into the stage, so they arrive during
+//     the step's arithmetic. The stage's 16-byte chunks are XOR-swizzled by row
 //     (the swizzle is applied to the source addresses, since lane i's bytes
 //     land at 16 i), so the column-wise K reads are free of bank conflicts.
 //   * When the page size is a power of two >= 16, a 16-token half lies in one
@@ -720,7 +722,7 @@ __device__ __forceinline__ void decode_split_body(const pa_decode_params& p, int
         }
     };
 
-    auto consume = [&](int s) {
+    auto consume_in = [&](int s) {
         if constexpr (DMA) {
             // With one step in flight, every vector memory operation
             // outstanding here belongs to this step: its Q and rows are in
@@ -781,6 +783,8 @@ __device__ __forceinline__ void decode_split_body(const pa_decode_params& p, int
                 }
             }
         }
+    };
+    auto consume_math = [&](int s) {
         // S^T[token][head] per 16-token half; lane (c, kb) gets tokens 4kb+i.
         float x[NH][4];
 #pragma unroll
@@ -918,10 +922,20 @@ __device__ __forceinline__ void decode_split_body(const pa_decode_params& p, int
     // it cannot count the outstanding loads and waits for all of them).
     static_assert(DEPTH >= 1 && DEPTH <= 4, "ring of 1 to 4 slots");
     auto advance = [&](int s) {
-        consume(s);
+        consume_in(s);
+        if constexpr (DMA) {
+            // The stage is in registers: the next step's rows land in it while
+            // this step's arithmetic runs (past the last step the loads are
+            // empty).
+            issue(s);
+            lookup(s);
+        }
+        consume_math(s);
         if (cursor_step<NG>(C, segs, seg_end) < 0) return false;
-        issue(s);
-        lookup(s);
+        if constexpr (!DMA) {
+            issue(s);
+            lookup(s);
+        }
         return true;
     };
     for (;;) {
