@@ -722,6 +722,8 @@ __device__ __forceinline__ void decode_split_body(const pa_decode_params& p, int
         }
     };
 
+    // A step's data into registers: the segment's Q at its first step, and on
+    // the stage paths the step's K / V rows out of the LDS stage.
     auto consume_in = [&](int s) {
         if constexpr (DMA) {
             // With one step in flight, every vector memory operation
@@ -784,6 +786,8 @@ __device__ __forceinline__ void decode_split_body(const pa_decode_params& p, int
             }
         }
     };
+    // A step's arithmetic on those registers: scores, online softmax, P V, and
+    // the segment's output or partial after its last step.
     auto consume_math = [&](int s) {
         // S^T[token][head] per 16-token half; lane (c, kb) gets tokens 4kb+i.
         float x[NH][4];
