@@ -8,6 +8,7 @@ flags and columns as the reference's bench/bench_decode.cu:1-16:
     python -m pa_amd.bench_decode copy                           attainable read bandwidth
     python -m pa_amd.bench_decode single    --batch B --len L    one configuration
     python -m pa_amd.bench_decode append    --batch B --len L    per-slot vs batched append
+    python -m pa_amd.bench_decode order     --batch B --len L    decode time per page placement
 
 Common flags: --hq 32 --hkv 8 --dim 128 --page 16 --iters 50 --dtype fp16|fp8
               --ctas N (0 = default grid) --contiguous-pages (no free-list shuffle)
@@ -370,7 +371,64 @@ def run_one(gpu: str, peak: float, fl: Flusher | None, s: Setup, ctas: int, iter
     return row
 
 
-MODES = ("sweep", "ctas", "pagesize", "capacity", "copy", "single", "append")
+def page_orders(batch: int, npg: int, page_bytes: int, seed: int = 7) -> dict:
+    """Placements of the batch's pages, each a permutation of the page ranks
+    0 .. batch * npg - 1 (rank r = row r // npg, page r % npg of an in-order
+    pool): entry (b, i) of the block table takes the perm[b * npg + i]-th page
+    of the pool in memory order."""
+    import numpy as np
+    n = batch * npg
+    rng = np.random.default_rng(seed)
+    order = {"memory_order": np.arange(n),
+             # page i of row b handed out as all rows grow together
+             "interleaved": (np.arange(npg)[None, :] * batch + np.arange(batch)[:, None]).reshape(-1),
+             "shuffled": rng.permutation(n)}
+    for span in (256 << 10, 2 << 20):
+        g = max(1, span // page_bytes)
+        if n % g:
+            continue
+        q = np.arange(n).reshape(-1, g)
+        name = f"{span >> 10}KiB" if span < (1 << 20) else f"{span >> 20}MiB"
+        order[f"shuffled_within_{name}"] = np.concatenate([rng.permutation(r) for r in q])
+        order[f"{name}_groups_shuffled"] = q[rng.permutation(len(q))].reshape(-1)
+    return order
+
+
+def page_order_rows(gpu: str, peak: float, fl, batch: int, length: int, hq: int, hkv: int, dim: int, page: int,
+                    fp8: bool, iters: int) -> list[dict]:
+    """Decode time at one page size under different placements of the same
+    pages. The pool is filled in memory order (no free-list shuffle); each row
+    points the step at a block table that permutes its pages (page_orders), so
+    the kernels read the same number of bytes from other addresses. The values
+    then belong to other rows' tokens: the rows time placement only."""
+    import numpy as np
+    import torch
+    s = Setup([length] * batch, hq, hkv, dim, page, fp8, shuffle=False)
+    npg = math.ceil(length / page)
+    own = np.stack([s.cache.block_table(b)[:npg] for b in range(batch)])
+    pages = np.sort(own.reshape(-1))   # the pool's pages in memory order
+    stride = s.params.block_table_stride
+    eb = 1 if fp8 else 2
+    page_bytes = hkv * page * dim * eb
+    rows = []
+    for name, perm in page_orders(batch, npg, page_bytes).items():
+        t = np.zeros((batch, stride), np.int32)
+        t[:, :npg] = pages[perm].reshape(batch, npg)
+        table = torch.from_numpy(t).cuda()
+        s.replan(0)
+        s.params.block_table = table.data_ptr()
+        ms = statistics.median(time_cold(fl, iters, s.run))
+        gbps = s.bytes() / (ms * 1e-3) / 1e9
+        row = dict(order=name, time_us=ms * 1e3, gbps=gbps, pct_peak=100.0 * gbps / peak)
+        print(f"{gpu},{core.kv_dtype_name(s.dtype)},{batch},{length},{page},{name},{row['time_us']:.2f},"
+              f"{gbps:.1f},{row['pct_peak']:.1f}", flush=True)
+        rows.append(row)
+        del table
+    s.close()
+    return rows
+
+
+MODES = ("sweep", "ctas", "pagesize", "capacity", "copy", "single", "append", "order")
 
 
 def main(argv: list[str] | None = None) -> int:
@@ -426,6 +484,10 @@ def main(argv: list[str] | None = None) -> int:
         print(HEADER)
         s = Setup([length] * batch, hq, hkv, dim, page, fp8, shuffle)
         run_one(gpu, peak, fl, s, ctas, iters)
+        return 0
+    if mode == "order":
+        print("gpu,dtype,batch,seq_len,page,order,time_us,gbps,pct_peak")
+        page_order_rows(gpu, peak, fl, batch, length, hq, hkv, dim, page, fp8, iters)
         return 0
     if mode == "ctas":
         print(HEADER)

@@ -67,7 +67,7 @@ def test_python_twin_help_needs_no_device():
     r = subprocess.run([sys.executable, "-m", "pa_amd.bench_decode", "--help"], capture_output=True, text=True,
                        timeout=120, cwd=cwd)
     assert r.returncode == 0
-    for mode in ("sweep", "ctas", "pagesize", "capacity", "copy", "single", "append"):
+    for mode in ("sweep", "ctas", "pagesize", "capacity", "copy", "single", "append", "order"):
         assert mode in r.stdout
     r = subprocess.run([sys.executable, "-m", "pa_amd.bench_decode", "nosuchmode"], capture_output=True, text=True,
                        timeout=120, cwd=cwd)
@@ -85,3 +85,43 @@ def test_bad_command_lines_exit_2_without_a_device():
         assert "usage: bench_decode" in proc.stderr
     out = _run("--help", "--batch=3")
     assert out.startswith("usage: bench_decode")
+
+
+def test_page_orders_are_permutations():
+    """The page placements of the `order` mode: each is a permutation of the
+    batch's pages; memory order is the identity, interleaved hands page i of
+    row b the rank i * batch + b, and the grouped shuffles keep every page in
+    its group (within) or every group whole (groups)."""
+    import sys
+    import numpy as np
+    sys.path.insert(0, str(ROOT / "paged-attention_amd"))
+    from pa_amd.bench_decode import page_orders
+    batch, npg, page_bytes = 8, 512, 32 << 10
+    n = batch * npg
+    orders = page_orders(batch, npg, page_bytes)
+    assert set(orders) == {"memory_order", "interleaved", "shuffled", "shuffled_within_256KiB",
+                           "256KiB_groups_shuffled", "shuffled_within_2MiB", "2MiB_groups_shuffled"}
+    for name, perm in orders.items():
+        assert np.array_equal(np.sort(perm), np.arange(n)), name
+    assert np.array_equal(orders["memory_order"], np.arange(n))
+    inter = orders["interleaved"].reshape(batch, npg)
+    assert inter[3, 5] == 5 * batch + 3
+    for span, g in (("256KiB", 8), ("2MiB", 64)):
+        w = orders[f"shuffled_within_{span}"].reshape(-1, g)
+        assert np.array_equal(w // g, np.repeat(np.arange(n // g)[:, None], g, axis=1))
+        q = orders[f"{span}_groups_shuffled"].reshape(-1, g)
+        assert np.array_equal(q - q[:, :1], np.repeat(np.arange(g)[None, :], n // g, axis=0))
+        assert np.array_equal(np.sort(q[:, 0] // g), np.arange(n // g))
+
+
+@pytest.mark.gpu
+def test_page_order_rows():
+    """`order` times one decode shape under every placement of its pages."""
+    import sys
+    cwd = ROOT / "paged-attention_amd"
+    r = subprocess.run([sys.executable, "-m", "pa_amd.bench_decode", "order", "--batch", "4", "--len", "2048",
+                        "--iters", "3", "--warm"], capture_output=True, text=True, timeout=300, cwd=cwd)
+    assert r.returncode == 0, r.stdout + r.stderr
+    rows = list(csv.DictReader(io.StringIO(r.stdout)))
+    assert {row["order"] for row in rows} >= {"memory_order", "interleaved", "shuffled"}
+    assert all(float(row["time_us"]) > 0 and row["page"] == "16" for row in rows)
