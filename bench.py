@@ -31,10 +31,12 @@ Fields of the JSON line:
                per step)
   workloads    the same figures (step, split kernel, cold) for C1, C3 (the
                FP8 target), C2 at 16-token pages and at one page per
-               sequence, C5 fp16 and FP8,
+               sequence, C2 at 16-token pages in memory order (free list
+               not shuffled), C5 fp16 and FP8,
                timed in the same run (each over max(K, 100) steps after
                max(W, 20) warm-ups); paging_overhead = C2 at 16-token pages
-               against one page per sequence; targets = the goals the
+               against one page per sequence (memory_order_*: the same with
+               the pages in memory order); targets = the goals the
                north star states, checked on these figures
   cpu_baseline the reference's cpu_attention (compiled from its source into
                oracle/_ref when that exists, else the oracle's restatement)
@@ -318,10 +320,12 @@ def device_report() -> dict:
 # Workloads timed beside the headline one (their figures go under
 # "workloads"): the CPU-runnable C1, the FP8 target C3, both ends of C2's
 # page-size comparison (paging overhead = C2 at 16-token pages against one
-# page per sequence, both timed the same way) and C5 in both dtypes.
-# (key, config, page size)
-EXTRA = [("c1", "c1", 16), ("c3", "c3", 16), ("c2_p16", "c2", 16), ("c2_p8192", "c2", 8192), ("c5", "c5", 16),
-         ("c5fp8", "c5fp8", 16)]
+# page per sequence, both timed the same way), C2's 16-token pages in memory
+# order (the pool's free list not shuffled: what the placement, not the paging,
+# costs) and C5 in both dtypes.
+# (key, config, page size, shuffled free list)
+EXTRA = [("c1", "c1", 16, True), ("c3", "c3", 16, True), ("c2_p16", "c2", 16, True), ("c2_p8192", "c2", 8192, True),
+         ("c2_p16_memory_order", "c2", 16, False), ("c5", "c5", 16, True), ("c5fp8", "c5fp8", 16, True)]
 
 
 def workload_figures(s, desc: str, steps: int, warmup: int, cold_iters: int, flusher) -> dict:
@@ -502,12 +506,15 @@ def main() -> None:
     if not args.no_extra:
         result["workloads"] = {}
         headline = (args.config, args.page_size)
-        for key, cfg, page in EXTRA:
-            if (cfg, page) == headline and key != "c2_p16":
+        for key, cfg, page, shuffled in EXTRA:
+            if (cfg, page) == headline and shuffled and key != "c2_p16":
                 continue
-            d = CONFIGS[cfg][0] if page == 16 else f"{CONFIGS[cfg][0].split(',')[0]}, {CONFIGS[cfg][0].split(', ')[1]}, {page}-token pages (one page per sequence)"
+            head = f"{CONFIGS[cfg][0].split(',')[0]}, {CONFIGS[cfg][0].split(', ')[1]}"
+            d = (CONFIGS[cfg][0] if page == 16 and shuffled else
+                 f"{head}, 16-token pages in memory order (free list not shuffled)" if page == 16 else
+                 f"{head}, {page}-token pages (one page per sequence)")
             print(f"# workload {key}: {d}", file=sys.stderr, flush=True)
-            kept[key] = bd.Setup(seq_lens_of(cfg), HQ, HKV, D, page, CONFIGS[cfg][4], shuffle=True, ctas=args.ctas)
+            kept[key] = bd.Setup(seq_lens_of(cfg), HQ, HKV, D, page, CONFIGS[cfg][4], shuffle=shuffled, ctas=args.ctas)
             # Each is timed over at least 100 steps after 20 warm-ups (K and W
             # count the headline's steps; a short window reads a few percent
             # slow while a new workload's first launches settle).
@@ -522,6 +529,14 @@ def main() -> None:
                 "split_pct": round(100 * (a["split_us"] / c["split_us"] - 1), 2),
                 "cold_pct": (round(100 * (a["cold_us"] / c["cold_us"] - 1), 2)
                              if "cold_us" in a and "cold_us" in c else None)}
+            if "c2_p16_memory_order" in w:
+                m = w["c2_p16_memory_order"]
+                # The same 16-token paging with the pages in memory order: the
+                # gap to the shuffled pool is what the random placement costs.
+                result["paging_overhead"]["memory_order_step_pct"] = round(
+                    100 * (m["us_per_step"] / c["us_per_step"] - 1), 2)
+                result["paging_overhead"]["memory_order_cold_pct"] = (
+                    round(100 * (m["cold_us"] / c["cold_us"] - 1), 2) if "cold_us" in m and "cold_us" in c else None)
         if args.config == "c2" and args.page_size == 16:
             result["targets"] = {
                 "c2_fp16_step_ge_80pct": result["pct_of_peak"] >= 80.0,
