@@ -1,7 +1,8 @@
-"""bench.py's one-line JSON contract: the fields, types and sub-objects the
-benchmark line carries (metric and unit, throughput value, timing, dtype,
-workload config, roofline of the dominant kernel, CPU baseline), and its
-refusal of multi-GPU runs."""
+"""bench.py's contract: one GPU only (--gpus N > 1 exits with a message,
+before anything touches a GPU), the driver's flags, and (on a GPU) the one
+JSON line with the fields, roofline and CPU baseline the driver reads."""
+
+from __future__ import annotations
 
 import json
 import pathlib
@@ -13,13 +14,32 @@ import pytest
 ROOT = pathlib.Path(__file__).resolve().parent.parent
 
 
-def test_multi_gpu_runs_are_refused():
-    """--gpus above 1 exits with status 2 and says why, before any device work."""
-    r = subprocess.run([sys.executable, "bench.py", "--gpus", "2", "--steps", "1", "--warmup", "0"],
-                       capture_output=True, text=True, timeout=120, cwd=ROOT)
-    assert r.returncode == 2
-    assert "one GPU" in r.stdout + r.stderr
-    assert r.stdout.strip() == "" or not r.stdout.strip().startswith("{")
+def _run(*args: str) -> subprocess.CompletedProcess:
+    return subprocess.run([sys.executable, str(ROOT / "bench.py"), *args], capture_output=True, text=True,
+                          timeout=120, cwd=ROOT)
+
+
+def test_more_than_one_gpu_exits_with_a_message():
+    for n in ("2", "8"):
+        r = _run("--gpus", n)
+        assert r.returncode == 2
+        assert "one GPU" in r.stderr
+        assert r.stdout == ""
+
+
+def test_world_size_above_one_exits_the_same_way():
+    import os
+    env = dict(os.environ, WORLD_SIZE="2", RANK="0", LOCAL_RANK="0")
+    r = subprocess.run([sys.executable, str(ROOT / "bench.py")], capture_output=True, text=True, timeout=120,
+                       cwd=ROOT, env=env)
+    assert r.returncode == 2 and "one GPU" in r.stderr
+
+
+def test_help_lists_the_driver_flags():
+    r = _run("--help")
+    assert r.returncode == 0
+    for flag in ("--gpus", "--steps", "--warmup", "--config"):
+        assert flag in r.stdout
 
 
 @pytest.mark.gpu
@@ -28,8 +48,8 @@ def test_bench_line_contract():
     headline metric as whole-job throughput, the dominant kernel's roofline
     (achieved, peak, fraction, traffic slot) and the CPU baseline (value,
     unit, cores, kind, sample)."""
-    r = subprocess.run([sys.executable, "bench.py", "--steps", "3", "--warmup", "1", "--no-copy", "--no-traffic",
-                        "--no-extra", "--cold-iters", "2", "--cpu-budget", "0.5"],
+    r = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--steps", "3", "--warmup", "1", "--no-copy",
+                        "--no-traffic", "--no-extra", "--cold-iters", "2", "--cpu-budget", "0.5"],
                        capture_output=True, text=True, timeout=600, cwd=ROOT)
     assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-2000:]
     lines = [ln for ln in r.stdout.splitlines() if ln.strip()]
