@@ -155,6 +155,52 @@ def test_append_batch_matches_sequential_appends(fp8):
         c.close()
 
 @pytest.mark.parametrize("fp8", DTYPES, ids=IDS)
+def test_append_batch_uniform_prefill_matches_sequential_appends(fp8):
+    """Batches whose entries all hold the same number of tokens (a uniform
+    prefill: the batched kernel finds every token's entry with its first guess,
+    entry t * entries / tokens) and one whose counts differ by one token (the
+    guess misses, the binary search finds the entry): pools, block tables and
+    lengths are bit-identical to per-slot appends of the same tokens."""
+    import torch
+    dt = pa_amd.FP8_E4M3 if fp8 else pa_amd.FP16
+    hkv, P, slots_n, max_pages = 4, 16, 5, 40
+    rng = np.random.default_rng(11)
+    caches = [pa_amd.PagedKVCache(160, P, hkv, D, slots_n, max_pages, dt, 4.0 / 448, 3.0 / 448) for _ in range(2)]
+    for c in caches:
+        c.shuffle_free_pages(9)
+        for _ in range(slots_n):
+            c.admit()
+    rounds = [([0, 1, 2, 3, 4], [37] * 5), ([4, 2, 0], [16] * 3), ([1, 3, 0, 2, 4], [33, 32, 33, 32, 33])]
+    for slots, counts in rounds:
+        total = sum(counts)
+        k = to_device(normal_f16(rng, (total, hkv, D)))
+        v = to_device(normal_f16(rng, (total, hkv, D)))
+        off = 0
+        for s_, n in zip(slots, counts):
+            assert caches[0].append(s_, k.data_ptr() + off * hkv * D * 2, v.data_ptr() + off * hkv * D * 2, n)
+            off += n
+        assert caches[1].append_batch(slots, counts, k, v)
+    torch.cuda.synchronize()
+    eb = 1 if fp8 else 2
+    nbytes = 160 * hkv * P * D * eb
+    view = (lambda a: a) if fp8 else (lambda a: a.view(np.uint16))
+    pools = [[view(d2h(getattr(c.params(), f), nbytes)) for f in ("k_cache", "v_cache")] for c in caches]
+    for s_ in range(slots_n):
+        t = caches[0].block_table(s_)
+        assert list(t) == list(caches[1].block_table(s_))
+        for h in range(hkv):
+            for f in range(2):
+                a = oracle.gather_raw(dt, pools[0][f], t, hkv, D, P, h, caches[0].seq_len(s_))
+                b = oracle.gather_raw(dt, pools[1][f], t, hkv, D, P, h, caches[1].seq_len(s_))
+                assert np.array_equal(a, b), f"slot {s_} head {h} {'kv'[f]}"
+    ta, la = _device_state(caches[0], range(slots_n), max_pages)
+    tb, lb = _device_state(caches[1], range(slots_n), max_pages)
+    assert np.array_equal(ta, tb) and np.array_equal(la, lb)
+    assert list(lb) == [37 + 16 + 33, 37 + 33, 37 + 16 + 32, 37 + 32, 37 + 16 + 33]
+    for c in caches:
+        c.close()
+
+@pytest.mark.parametrize("fp8", DTYPES, ids=IDS)
 def test_cache_plan_subset_of_slots_in_any_order(fp8):
     """PagedKVCache::plan(slots) (paged_kv_cache.cu:173-191): batch row i reads
     cache slot slots[i]. A released and re-admitted slot, a subset of the
