@@ -1032,17 +1032,24 @@ __global__ __launch_bounds__(64 * WAVES) void decode_merge_kernel(const pa_decod
         m     = mn;
     }
     // Combine (m, den, acc) states: lanes of the same dims, then waves.
+    // Within a row of 16 lanes the partner comes from a DPP rotation by o
+    // (rotations by 4 and then 8 combine the same four lanes as exchanges
+    // with lanes 4 and 8 apart, without an LDS round trip); across rows from
+    // a lane exchange.
     auto scale_to = [](float mi, float mt) { return mi == -INFINITY ? 0.f : exp2_fast(mi - mt); };
+    auto partner = [](float x, int o) {
+        return o == 4 ? dpp_f32<0x124>(x) : o == 8 ? dpp_f32<0x128>(x) : __shfl_xor(x, o);   // row_ror:4 / :8
+    };
 #pragma unroll
     for (int o = LPS; o < 64; o <<= 1) {
-        const float m2 = __shfl_xor(m, o);
+        const float m2 = partner(m, o);
         const float mt = fmaxf(m, m2);
         const float f1 = scale_to(m, mt), f2 = scale_to(m2, mt);
-        acc.x = acc.x * f1 + __shfl_xor(acc.x, o) * f2;
-        acc.y = acc.y * f1 + __shfl_xor(acc.y, o) * f2;
-        acc.z = acc.z * f1 + __shfl_xor(acc.z, o) * f2;
-        acc.w = acc.w * f1 + __shfl_xor(acc.w, o) * f2;
-        den   = den * f1 + __shfl_xor(den, o) * f2;
+        acc.x = acc.x * f1 + partner(acc.x, o) * f2;
+        acc.y = acc.y * f1 + partner(acc.y, o) * f2;
+        acc.z = acc.z * f1 + partner(acc.z, o) * f2;
+        acc.w = acc.w * f1 + partner(acc.w, o) * f2;
+        den   = den * f1 + partner(den, o) * f2;
         m     = mt;
     }
     if (lane < LPS) acc_lds[wave][lane] = acc;
