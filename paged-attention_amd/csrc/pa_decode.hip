@@ -1031,14 +1031,24 @@ __global__ __launch_bounds__(64 * WAVES) void decode_merge_kernel(const pa_decod
         den   = fmaf(den, f, wgt);
         m     = mn;
     }
-    // Combine (m, den, acc) states: lanes of the same dims, then waves.
-    // Within a row of 16 lanes the partner comes from a DPP rotation by o
-    // (rotations by 4 and then 8 combine the same four lanes as exchanges
-    // with lanes 4 and 8 apart, without an LDS round trip); across rows from
-    // a lane exchange.
+    // Combine (m, den, acc) states: lanes of the same dims, then waves. The
+    // partner state comes without an LDS round trip: within a row of 16
+    // lanes from a DPP rotation by o (rotations by 4 and then 8 combine the
+    // same four lanes as exchanges with lanes 4 and 8 apart), across rows
+    // from gfx950's row / half swaps (v_permlane16_swap, v_permlane32_swap:
+    // with the value as both operands, the first result holds lane i - o in
+    // the upper row / half, the second lane i + o in the lower one).
     auto scale_to = [](float mi, float mt) { return mi == -INFINITY ? 0.f : exp2_fast(mi - mt); };
-    auto partner = [](float x, int o) {
-        return o == 4 ? dpp_f32<0x124>(x) : o == 8 ? dpp_f32<0x128>(x) : __shfl_xor(x, o);   // row_ror:4 / :8
+    auto partner = [lane](float x, int o) {
+        const unsigned u = __builtin_bit_cast(unsigned, x);
+        if (o == 4) return dpp_f32<0x124>(x);   // row_ror:4
+        if (o == 8) return dpp_f32<0x128>(x);   // row_ror:8
+        if (o == 16) {
+            const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+            return __builtin_bit_cast(float, (lane & 16) ? r[0] : r[1]);
+        }
+        const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+        return __builtin_bit_cast(float, (lane & 32) ? r[0] : r[1]);
     };
 #pragma unroll
     for (int o = LPS; o < 64; o <<= 1) {
