@@ -32,7 +32,7 @@ Fields of the JSON line:
   workloads    the same figures (step, split kernel, cold) for C1, C3 (the
                FP8 target), C2 at 16-token pages and at one page per
                sequence, C2 at 16-token pages in memory order (free list
-               not shuffled), C5 fp16 and FP8,
+               not shuffled), the ragged C4, C5 fp16 and FP8,
                timed in the same run (each over max(K, 100) steps after
                max(W, 20) warm-ups); paging_overhead = C2 at 16-token pages
                against one page per sequence (memory_order_*: the same with
@@ -266,6 +266,9 @@ def measure_traffic(args) -> dict | None:
     import csv
     import shutil
     import tempfile
+    if profiler_preloaded():
+        print("# traffic passes skipped: this process runs under a profiler", file=sys.stderr, flush=True)
+        return None
     prof = shutil.which("rocprofv3")
     if not prof:
         return None
@@ -301,20 +304,51 @@ def measure_traffic(args) -> dict | None:
     return out
 
 
-def device_report() -> dict:
-    """The box's own figures for the GPU (`amd-smi static`), so the line carries
-    the reported HBM bandwidth beside the published 8 TB/s it is priced against.
-    Runs as a child process before this process touches the GPU."""
+def profiler_preloaded(env=None) -> bool:
+    """True when this process runs under a profiler's preloaded library
+    (rocprofv3 sets LD_PRELOAD and ROCPROF_* variables). A child process would
+    inherit the preload, which initializes the GPU before the child's own
+    program starts; `rocprofv3` is itself a `#!/usr/bin/env python3` script, so
+    starting one from here would make a GPU-initialized process exec. bench.py
+    therefore starts no child process at all in that case."""
+    env = os.environ if env is None else env
+    if "rocprof" in env.get("LD_PRELOAD", "").lower():
+        return True
+    return any(k.startswith(("ROCPROF_", "ROCPROFILER_")) for k in env)
+
+
+# hipDeviceAttribute_t values (hip/hip_runtime_api.h): global memory bus width
+# in bits and peak memory clock in kHz.
+_HIP_ATTR_MEMORY_BUS_WIDTH = 59
+_HIP_ATTR_MEMORY_CLOCK_RATE = 60
+
+
+def device_report(dev: int = 0) -> dict:
+    """The device's own figures from the HIP runtime in this process (no child
+    process): name, ISA, compute units and HBM size from hipGetDeviceProperties,
+    and the DRAM peak the device reports, memory clock x bus width x 2 (double
+    data rate), derived as bench_decode.cu:87-100 derives it. The line carries
+    that reported peak beside the published 8 TB/s it is priced against."""
     try:
-        proc = subprocess.run(["amd-smi", "static", "--gpu", "0", "--json"], capture_output=True, text=True,
-                              timeout=60)
-        g = json.loads(proc.stdout)["gpu_data"][0]
-        vram, asic = g["vram"], g["asic"]
-        return {"name": asic.get("market_name"), "arch": asic.get("target_graphics_version"),
-                "cus": asic.get("num_compute_units"), "hbm": f"{vram.get('type')} {vram['size']['value']} MB",
-                "reported_max_bandwidth_gbps": vram["max_bandwidth"]["value"], "source": "amd-smi static"}
-    except (OSError, ValueError, KeyError, IndexError, TypeError, subprocess.SubprocessError) as e:
-        return {"source": f"amd-smi unavailable ({type(e).__name__})"}
+        import torch
+        if not torch.cuda.is_available():
+            return {"source": "no HIP device"}
+        props = torch.cuda.get_device_properties(dev)
+        hip = ctypes.CDLL("libamdhip64.so")
+        hip.hipDeviceGetAttribute.argtypes = [ctypes.POINTER(ctypes.c_int), ctypes.c_int, ctypes.c_int]
+        hip.hipDeviceGetAttribute.restype = ctypes.c_int
+
+        def attr(a: int) -> int:
+            v = ctypes.c_int(0)
+            return v.value if hip.hipDeviceGetAttribute(ctypes.byref(v), a, dev) == 0 else 0
+
+        clock_khz, bus_bits = attr(_HIP_ATTR_MEMORY_CLOCK_RATE), attr(_HIP_ATTR_MEMORY_BUS_WIDTH)
+        return {"name": props.name, "arch": props.gcnArchName.split(":")[0], "cus": props.multi_processor_count,
+                "hbm_bytes": int(props.total_memory), "memory_clock_khz": clock_khz, "memory_bus_bits": bus_bits,
+                "reported_peak_gbps": round(2.0 * clock_khz * 1e3 * bus_bits / 8 / 1e9, 1),
+                "source": "HIP runtime (hipGetDeviceProperties, hipDeviceGetAttribute)"}
+    except (OSError, RuntimeError, AttributeError, ValueError) as e:
+        return {"source": f"HIP device query failed ({type(e).__name__})"}
 
 
 # Workloads timed beside the headline one (their figures go under
@@ -322,10 +356,11 @@ def device_report() -> dict:
 # page-size comparison (paging overhead = C2 at 16-token pages against one
 # page per sequence, both timed the same way), C2's 16-token pages in memory
 # order (the pool's free list not shuffled: what the placement, not the paging,
-# costs) and C5 in both dtypes.
+# costs), the ragged C4 and C5 in both dtypes.
 # (key, config, page size, shuffled free list)
 EXTRA = [("c1", "c1", 16, True), ("c3", "c3", 16, True), ("c2_p16", "c2", 16, True), ("c2_p8192", "c2", 8192, True),
-         ("c2_p16_memory_order", "c2", 16, False), ("c5", "c5", 16, True), ("c5fp8", "c5fp8", 16, True)]
+         ("c2_p16_memory_order", "c2", 16, False), ("c4", "c4", 16, True), ("c5", "c5", 16, True),
+         ("c5fp8", "c5fp8", 16, True)]
 
 
 def workload_figures(s, desc: str, steps: int, warmup: int, cold_iters: int, flusher) -> dict:
@@ -382,16 +417,16 @@ def main() -> None:
               file=sys.stderr)
         sys.exit(2)
 
-    # The counter passes and the device query run before this process
-    # initializes the GPU.
+    # The counter passes (child processes) run before this process initializes
+    # the GPU, and not at all under a profiler.
     traffic = None if args.no_traffic else measure_traffic(args)
-    device = device_report()
 
     import torch
     if not torch.cuda.is_available():
         print("bench.py: needs a GPU (cuda:0)", file=sys.stderr)
         sys.exit(1)
     torch.cuda.set_device(0)
+    device = device_report(0)
     from pa_amd import bench_decode as bd
     import pa_amd
     pa_amd._lib.load()

@@ -80,6 +80,8 @@ typedef struct pa_decode_params {
     int32_t         block_merge;       /* 1: every split (row, kv head) lies in one block of
                                           8 work units and the split kernel merges it
                                           (needs_merge is then 0). Set by bind. */
+    int32_t         num_segments;      /* segments of the bound plan (0 = unknown); sizes the
+                                          partial workspace. Set by bind. */
 } pa_decode_params;
 
 /* Thread-local message describing the last failed call ("" if none). */
@@ -162,15 +164,19 @@ pa_status pa_decode_merge(int dtype, const pa_decode_params* p, void* stream);
  * that forbid hipMalloc): the same split and merge launches, but the partial
  * workspace of rows split across blocks lives in a fixed 32 MiB device array
  * of the library (one per GPU, held until the process ends) instead of
- * p->partial_out / p->partial_lse, which are ignored. num_segments must be
- * the bound plan's segment count (pa_plan_num_segments): the kernels write
- * that many partials, so a smaller count would let them write past the array
- * (counts below batch * num_kv_heads or p->max_item_segments are refused with
- * PA_ERR_INVALID_ARGUMENT); a plan whose workspace,
+ * p->partial_out / p->partial_lse, which are ignored. p must be bound to a
+ * device plan (pa_device_plan_bind records the plan's segment count in
+ * p->num_segments), and num_segments must equal that count
+ * (pa_plan_num_segments); anything else is refused with
+ * PA_ERR_INVALID_ARGUMENT before any launch. A plan whose workspace,
  * num_segments * group * (head_dim + 1) * 4 bytes, exceeds 32 MiB is refused
- * with PA_ERR_LENGTH (plans merged in the split kernel, p->block_merge = 1,
- * need none). Allocates nothing. Calls on one GPU share its array: calls that
- * overlap on one GPU (two streams, two threads) race. */
+ * with PA_ERR_LENGTH; plans without split rows, or merged in the split kernel
+ * (p->block_merge = 1), need none. The array's address is looked up by the
+ * plan upload on the device (so a first call made under graph capture needs
+ * no lookup); a first call on a device that has seen no upload looks it up
+ * itself, and refuses to while its stream is being captured. Allocates
+ * nothing. Calls on one GPU share its array: calls that overlap on one GPU
+ * (two streams, two threads) race. */
 pa_status pa_decode_static(int dtype, const pa_decode_params* p, int num_segments, void* stream);
 
 /* paged_kv_cache.cu:15-39 quantize<> + append_kernel, launch at :122-131:

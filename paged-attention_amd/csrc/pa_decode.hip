@@ -993,6 +993,8 @@ template <int G, int WAVES, int DS>
 __global__ __launch_bounds__(64 * WAVES) void decode_merge_kernel(const pa_decode_params p) {
     constexpr int LPS = DS / 4;      // lanes per segment
     constexpr int SPW = 64 / LPS;    // segments per wave per pass
+    // The combine below exchanges lanes 4, 8, 16 and 32 apart only.
+    static_assert(LPS >= 4 && LPS <= 32 && (LPS & (LPS - 1)) == 0, "dim slices of 16, 32, 64 or 128");
     const int hqi  = blockIdx.x;
     const int b    = blockIdx.y;
     const int d0   = blockIdx.z * DS;

@@ -61,6 +61,7 @@ struct pa_device_plan {
     int      num_ctas    = 0;
     int      needs_merge = 0;
     int      max_item_segments = 0;
+    int      num_segments = 0;
     bool     block_merge = false;
     pa_stage_pool staging;
 };
@@ -145,6 +146,13 @@ void device_plan_upload(pa_device_plan& dp, const pa_plan& plan, int group, int 
 void device_plan_bind(const pa_device_plan& dp, pa_decode_params& p);
 void device_plan_free(pa_device_plan& dp);
 void decode_impl(int dtype, const pa_decode_params& p, hipStream_t s, bool split, bool merge);
+
+// ---- allocation-free decode (pa_scratch.hip)
+// Looks up the device address of pa_decode_static's static scratch array on
+// the current device, once per device. Plan uploads call it, so the lookup
+// (which may load the library's code object onto the device) happens at set-up,
+// outside any graph capture of the decode that follows.
+void scratch_prepare();
 
 // ---- page pool (pa_pool.cpp)
 // Entry i of a batched append: the slot's length before it, and the table

@@ -162,6 +162,7 @@ void device_plan_upload(pa_device_plan& dp, const pa_plan& plan, int group, int 
                         const int32_t* extra, size_t n_extra) {
     if (group <= 0 || head_dim <= 0) throw std::invalid_argument("upload: bad group or head_dim");
     if (n_extra && !extra) throw std::invalid_argument("upload: extra ints are null");
+    scratch_prepare();
     const size_t nseg = plan.segments.size() / 4;
     // The kernels read a 16-token group from one page run (page sizes >= 16) or
     // one 1 KiB part from one page: a segment may only start on a group boundary.
@@ -210,6 +211,7 @@ void device_plan_upload(pa_device_plan& dp, const pa_plan& plan, int group, int 
     }
     dp.partial_lse = dp.partial_out ? dp.partial_out + rows * head_dim : nullptr;
     dp.num_ctas = plan.num_ctas;
+    dp.num_segments = static_cast<int>(nseg);
     // Block-level merge: the split kernel merges a split row itself when all
     // its segments lie in one block of kBlockUnits units. It needs every split
     // segment to be its unit's first or last (true of every make_plan cut) and
@@ -248,6 +250,7 @@ void device_plan_bind(const pa_device_plan& dp, pa_decode_params& p) {
     p.partial_lse    = dp.partial_lse;
     p.max_item_segments = dp.max_item_segments;
     p.block_merge       = dp.block_merge ? 1 : 0;
+    p.num_segments      = dp.num_segments;
 }
 void device_plan_free(pa_device_plan& dp) {
     free_stages(dp.staging);

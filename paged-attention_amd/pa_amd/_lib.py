@@ -73,6 +73,7 @@ class DecodeParams(ctypes.Structure):
         ("partial_lse", ctypes.c_void_p),
         ("max_item_segments", ctypes.c_int32),
         ("block_merge", ctypes.c_int32),
+        ("num_segments", ctypes.c_int32),
     ]
 
 

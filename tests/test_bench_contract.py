@@ -35,6 +35,51 @@ def test_world_size_above_one_exits_the_same_way():
     assert r.returncode == 2 and "one GPU" in r.stderr
 
 
+def _no_children(monkeypatch):
+    """Makes any attempt to start a child process fail the test."""
+    import os
+
+    def refuse(*a, **k):
+        raise AssertionError(f"child process started: {a[:1]}")
+    monkeypatch.setattr(subprocess, "Popen", refuse)
+    for name in ("system", "execv", "execve", "execvp", "execvpe", "posix_spawn", "posix_spawnp", "fork"):
+        if hasattr(os, name):
+            monkeypatch.setattr(os, name, refuse)
+
+
+def test_profiler_preload_is_detected():
+    import bench
+    assert bench.profiler_preloaded({"LD_PRELOAD": "/opt/rocm/lib/rocprofiler-sdk/librocprofiler-sdk-tool.so"})
+    assert bench.profiler_preloaded({"ROCPROF_KERNEL_TRACE": "1"})
+    assert bench.profiler_preloaded({"ROCPROFILER_LIBRARY_CTOR": "1"})
+    assert not bench.profiler_preloaded({"LD_PRELOAD": "", "PATH": "/usr/bin"})
+    assert not bench.profiler_preloaded({})
+
+
+def test_no_child_process_under_a_profiler(monkeypatch):
+    """Under a profiler's preload every child would start GPU-initialized (and
+    rocprofv3 is a `#!/usr/bin/env python3` script, i.e. an exec): the traffic
+    passes are skipped and nothing is started."""
+    import argparse
+
+    import bench
+    _no_children(monkeypatch)
+    monkeypatch.setenv("LD_PRELOAD", "/opt/rocm/lib/rocprofiler-sdk/librocprofiler-sdk-tool.so")
+    args = argparse.Namespace(config="c2", page_size=16, ctas=0)
+    assert bench.measure_traffic(args) is None
+
+
+def test_device_report_starts_no_child_process(monkeypatch):
+    """The device facts come from the HIP runtime in-process (no amd-smi, which
+    is itself a `#!/usr/bin/env python3` script); without a device it says so."""
+    import bench
+    _no_children(monkeypatch)
+    monkeypatch.setenv("ROCPROF_KERNEL_TRACE", "1")
+    d = bench.device_report(0)
+    assert isinstance(d, dict) and "source" in d
+    assert "amd-smi" not in json.dumps(d)
+
+
 def test_help_lists_the_driver_flags():
     r = _run("--help")
     assert r.returncode == 0

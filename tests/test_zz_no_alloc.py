@@ -38,28 +38,56 @@ def _params(q, k, v, table, lens, hq, hkv, ks, vs, dplan):
 
 
 def test_decode_static_refuses_oversized_plans_without_a_device():
-    """A plan whose partial workspace exceeds the 32 MiB array is refused with
-    PA_ERR_LENGTH, and null params, a segment count no plan of the params can
-    have (zero for a non-empty grid, fewer than batch x kv heads, fewer than the
-    plan's most per row), an unknown dtype or an unsupported head_dim with
-    PA_ERR_INVALID_ARGUMENT, before the library looks up the array or launches
-    anything."""
+    """The workspace is sized from the bound plan's own segment count
+    (params.num_segments, set by DevicePlan.bind). A plan whose partial
+    workspace exceeds the 32 MiB array is refused with PA_ERR_LENGTH; null
+    params, params not bound to a plan (num_segments 0 for a non-empty grid), a
+    caller's count that differs from the bound one (under- or overstated), split
+    rows with neither merge set, an unknown dtype or an unsupported head_dim
+    with PA_ERR_INVALID_ARGUMENT; all before the library looks up the array or
+    launches anything."""
     lib = _lib.load()
     p = pa_amd.DecodeParams()
     p.num_q_heads, p.num_kv_heads, p.head_dim, p.num_ctas, p.batch = 32, 8, D, 2048, 4
     per_seg = 4 * (D + 1) * 4                         # group 4: 4 rows of head_dim + 1 floats
     too_many = SCRATCH_BYTES // per_seg + 1
+    p.num_segments, p.needs_merge = too_many, 1
     assert lib.pa_decode_static(0, ctypes.byref(p), too_many, None) == _lib.PA_ERR_LENGTH
     assert b"static scratch" in lib.pa_last_error()
     assert lib.pa_decode_static(0, None, 10, None) == _lib.PA_ERR_INVALID_ARGUMENT
+    # An understated count: the kernels would write the bound plan's partials.
+    p.num_segments = 2048
+    for wrong in (2047, 1000, 32, 0, 4096):
+        assert lib.pa_decode_static(0, ctypes.byref(p), wrong, None) == _lib.PA_ERR_INVALID_ARGUMENT, wrong
+        assert b"differs from the bound plan" in lib.pa_last_error()
+    p.num_segments = 0                                  # not bound
     assert lib.pa_decode_static(0, ctypes.byref(p), 0, None) == _lib.PA_ERR_INVALID_ARGUMENT
-    assert lib.pa_decode_static(0, ctypes.byref(p), 31, None) == _lib.PA_ERR_INVALID_ARGUMENT   # < 4 x 8 rows
-    p.max_item_segments = 64
-    assert lib.pa_decode_static(0, ctypes.byref(p), 40, None) == _lib.PA_ERR_INVALID_ARGUMENT   # < one row's
-    p.max_item_segments = 0
-    assert lib.pa_decode_static(5, ctypes.byref(p), 10, None) == _lib.PA_ERR_INVALID_ARGUMENT
+    assert b"not bound" in lib.pa_last_error()
+    p.num_segments, p.needs_merge, p.block_merge = 2048, 0, 0   # split rows, no merge
+    assert lib.pa_decode_static(0, ctypes.byref(p), 2048, None) == _lib.PA_ERR_INVALID_ARGUMENT
+    p.needs_merge = 1
+    assert lib.pa_decode_static(5, ctypes.byref(p), 2048, None) == _lib.PA_ERR_INVALID_ARGUMENT
     p.head_dim = 64
-    assert lib.pa_decode_static(0, ctypes.byref(p), 10, None) == _lib.PA_ERR_INVALID_ARGUMENT
+    assert lib.pa_decode_static(0, ctypes.byref(p), 2048, None) == _lib.PA_ERR_INVALID_ARGUMENT
+
+
+def test_decode_static_sizes_no_workspace_for_unsplit_or_block_merged_plans():
+    """Plans that write no partial to HBM need no workspace, however many
+    segments they have: every segment whole (2048 rows x 8 kv heads = 16384
+    whole segments, 33.8 MB at 4 x 129 floats each) or every split row merged
+    in LDS. Neither is refused for size; without a device the call then stops
+    at the device step (or, with one, at the null pointers of these params)."""
+    lib = _lib.load()
+    p = pa_amd.DecodeParams()
+    p.num_q_heads, p.num_kv_heads, p.head_dim, p.num_ctas, p.batch = 32, 8, D, 2048, 2048
+    assert 16384 * 4 * (D + 1) * 4 > SCRATCH_BYTES
+    p.num_segments, p.needs_merge, p.block_merge = 16384, 0, 0
+    st = lib.pa_decode_static(0, ctypes.byref(p), 16384, None)
+    assert st not in (_lib.PA_OK, _lib.PA_ERR_LENGTH) and b"static scratch" not in lib.pa_last_error()
+    p.batch = 4
+    p.num_segments, p.needs_merge, p.block_merge = 16384, 0, 1
+    st = lib.pa_decode_static(0, ctypes.byref(p), 16384, None)
+    assert st not in (_lib.PA_OK, _lib.PA_ERR_LENGTH) and b"static scratch" not in lib.pa_last_error()
 
 
 @pytest.mark.gpu
@@ -91,18 +119,15 @@ def test_decode_static_matches_decode_on_two_calls(fp8):
         p_st.partial_lse = None
         out_st.fill_(float("nan"))
         stream = torch.cuda.current_stream().cuda_stream
+        assert p_st.num_segments == nseg                 # recorded by bind
+        # A count that disagrees with the bound plan launches nothing.
+        assert lib.pa_decode_static(dt, ctypes.byref(p_st), nseg - 1, stream) == _lib.PA_ERR_INVALID_ARGUMENT
+        torch.cuda.synchronize()
+        assert torch.isnan(out_st.float()).all()
         assert lib.pa_decode(dt, ctypes.byref(p_ref), stream) == _lib.PA_OK
         assert lib.pa_decode_static(dt, ctypes.byref(p_st), nseg, stream) == _lib.PA_OK, lib.pa_last_error()
         torch.cuda.synchronize()
         assert torch.equal(out_st.view(torch.int16), out_ref.view(torch.int16)), f"call {i + 1} differs"
-        if merged:
-            # Merged in LDS: no workspace, so even a segment count past the
-            # array's capacity is accepted.
-            too_many = SCRATCH_BYTES // ((hq // hkv) * (D + 1) * 4) + 1
-            out_st.fill_(float("nan"))
-            assert lib.pa_decode_static(dt, ctypes.byref(p_st), too_many, stream) == _lib.PA_OK
-            torch.cuda.synchronize()
-            assert torch.equal(out_st.view(torch.int16), out_ref.view(torch.int16))
         kb = k.view(torch.uint8).cpu().numpy() if fp8 else k.view(torch.int16).cpu().numpy().view(np.uint16)
         vb = v.view(torch.uint8).cpu().numpy() if fp8 else v.view(torch.int16).cpu().numpy().view(np.uint16)
         ref = oracle.paged_decode(dt, q.view(torch.int16).cpu().numpy().view(np.uint16), kb, vb, table.cpu().numpy(),
@@ -138,9 +163,6 @@ def test_decode_static_graph_replays_match_eager():
     st = torch.cuda.Stream()
     with torch.cuda.stream(st):
         h = st.cuda_stream
-        # Eager first: the array's address is looked up outside the capture.
-        assert lib.pa_decode_static(0, ctypes.byref(p_st), nseg, h) == _lib.PA_OK, lib.pa_last_error()
-        torch.cuda.synchronize()
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph, stream=st):
             status = lib.pa_decode_static(0, ctypes.byref(p_st), nseg, torch.cuda.current_stream().cuda_stream)
@@ -155,3 +177,64 @@ def test_decode_static_graph_replays_match_eager():
             assert lib.pa_decode_static(0, ctypes.byref(p_other), nseg, h) == _lib.PA_OK
             torch.cuda.synchronize()
             assert torch.equal(out_st.view(torch.int16), out_ref.view(torch.int16)), f"replay {rep} differs"
+
+
+_FIRST_CALL_IN_CAPTURE = r"""
+import ctypes, sys
+sys.path[:0] = [sys.argv[1], sys.argv[2], sys.argv[3]]
+import torch
+import pa_amd
+from pa_amd import _lib
+from helpers import D, paged_inputs
+torch.cuda.set_device(0)
+lib = _lib.load()
+hq, hkv, lens = 32, 8, [1024] * 4
+q, k, v, table, ks, vs = paged_inputs(len(lens), lens, hq, hkv, 16, False, seed=78)
+plan = pa_amd.make_plan(pa_amd.FP16, lens, hq, hkv, D, 0)
+dplan = pa_amd.DevicePlan()
+dplan.upload(plan, hq // hkv, D)          # set-up: looks up the array's address
+def params(out):
+    p = pa_amd.DecodeParams()
+    p.q, p.k_cache, p.v_cache, p.block_table = q.data_ptr(), k.data_ptr(), v.data_ptr(), table.data_ptr()
+    p.out = out.data_ptr()
+    p.block_table_stride = table.size(1)
+    p.batch, p.num_q_heads, p.num_kv_heads, p.head_dim, p.page_size = len(lens), hq, hkv, D, 16
+    p.sm_scale, p.k_scale, p.v_scale = pa_amd.sm_scale(D), ks, vs
+    dplan.bind(p)
+    return p
+out_ref, out_st = torch.empty_like(q), torch.zeros_like(q)
+p_ref, p_st = params(out_ref), params(out_st)
+assert p_ref.needs_merge == 1
+st = torch.cuda.Stream()
+with torch.cuda.stream(st):
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=st):
+        status = lib.pa_decode_static(0, ctypes.byref(p_st), len(plan.segments),
+                                      torch.cuda.current_stream().cuda_stream)
+    assert status == _lib.PA_OK, lib.pa_last_error()
+    assert lib.pa_decode(0, ctypes.byref(p_ref), st.cuda_stream) == _lib.PA_OK
+    torch.cuda.synchronize()
+    for rep in range(3):
+        out_st.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out_st.view(torch.int16), out_ref.view(torch.int16)), rep
+print("first call in capture: ok", flush=True)
+"""
+
+
+@pytest.mark.gpu
+@pytest.mark.usefixtures("gpu_device")
+def test_decode_static_first_call_inside_a_capture():
+    """In a fresh process, the entry point's first call is made inside a HIP
+    graph capture: the plan upload before it has already looked up the array,
+    so the capture needs no lookup, and every replay equals eager pa_decode."""
+    import pathlib
+    import subprocess
+    import sys
+    root = pathlib.Path(__file__).resolve().parent.parent
+    print("# child: first pa_decode_static call inside a graph capture (4 x 1024 fp16)", flush=True)
+    r = subprocess.run([sys.executable, "-c", _FIRST_CALL_IN_CAPTURE, str(root), str(root / "paged-attention_amd"),
+                        str(root / "tests")], capture_output=True, text=True, timeout=110)
+    assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-3000:]
+    assert "first call in capture: ok" in r.stdout
