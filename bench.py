@@ -343,9 +343,18 @@ def device_report(dev: int = 0) -> dict:
             return v.value if hip.hipDeviceGetAttribute(ctypes.byref(v), a, dev) == 0 else 0
 
         clock_khz, bus_bits = attr(_HIP_ATTR_MEMORY_CLOCK_RATE), attr(_HIP_ATTR_MEMORY_BUS_WIDTH)
-        return {"name": props.name, "arch": props.gcnArchName.split(":")[0], "cus": props.multi_processor_count,
-                "hbm_bytes": int(props.total_memory), "memory_clock_khz": clock_khz, "memory_bus_bits": bus_bits,
-                "reported_peak_gbps": round(2.0 * clock_khz * 1e3 * bus_bits / 8 / 1e9, 1),
+        arch = props.gcnArchName.split(":")[0]
+        # The runtime's name is generic on these boxes (the marketing name needs
+        # libdrm's id table): the ISA name and PCI device id stand in for it.
+        name = props.name if props.name and props.name != "AMD Radeon Graphics" else f"AMD {arch}"
+        return {"name": name, "arch": arch, "pci_device_id": f"0x{props.pci_device_id:04x}",
+                "cus": props.multi_processor_count, "hbm_bytes": int(props.total_memory),
+                "memory_clock_khz": clock_khz, "memory_bus_bits": bus_bits,
+                # bench_decode.cu:87-100's formula. HBM3E moves 8 Gb/s per pin
+                # (8192 bits x 8 Gb/s / 8 = 8.2 TB/s, the published 8 TB/s), while
+                # the runtime reports a 2 GHz memory clock, so on MI355X the
+                # formula gives half of that.
+                "formula_peak_gbps": round(2.0 * clock_khz * 1e3 * bus_bits / 8 / 1e9, 1),
                 "source": "HIP runtime (hipGetDeviceProperties, hipDeviceGetAttribute)"}
     except (OSError, RuntimeError, AttributeError, ValueError) as e:
         return {"source": f"HIP device query failed ({type(e).__name__})"}

@@ -134,4 +134,15 @@ def build_torch_ext(verbose: bool = False) -> pathlib.Path:
 
 
 if __name__ == "__main__":
-    print(build(verbose="-v" in sys.argv))
+    import argparse
+    ap = argparse.ArgumentParser(description="Builds libpa_decode.so for gfx950. With -D, a comparison build of the "
+                                             "kernels' compile-time knobs (e.g. -D PA_STAGE_SWIZZLE=0) into --lib; "
+                                             "load it with PA_DECODE_LIB=<path>.")
+    ap.add_argument("-v", "--verbose", action="store_true")
+    ap.add_argument("-D", dest="defines", action="append", default=[], metavar="NAME=VALUE")
+    ap.add_argument("--lib", type=pathlib.Path, default=None, help="output library (default lib/libpa_decode.so)")
+    a = ap.parse_args()
+    if a.defines and a.lib is None:
+        ap.error("a build with -D needs its own --lib path (lib/libpa_decode.so stays the product build)")
+    obj = None if a.lib is None else OBJ_DIR / ("variant_" + a.lib.stem)
+    print(build(verbose=a.verbose, defines=a.defines, lib=a.lib, obj_dir=obj))

@@ -120,6 +120,13 @@
 #ifndef PA_FP16_LDS_STAGE
 #define PA_FP16_LDS_STAGE 0
 #endif
+// 1: the LDS stage stores 16-byte chunk j of row r at chunk position
+// j ^ (r % chunks per row), so that the column-wise reads of the MFMA lane
+// layouts hit distinct banks; 0: chunks in natural order (the comparison build
+// behind the bank-conflict counters).
+#ifndef PA_STAGE_SWIZZLE
+#define PA_STAGE_SWIZZLE 1
+#endif
 // 1: every LDS-staged path fills the stage with LDS-destination loads
 // (buffer / global_load_dwordx4 ... lds: 16 bytes per lane land at M0 + 16 *
 // lane, no VGPRs, no ds_write), one step in flight; 0: loads into VGPRs, then
@@ -147,6 +154,7 @@ template <int EB> struct Tune {
 static_assert(Tune<2>::step == 16 || Tune<2>::step == 32, "fp16 step must be 16 or 32");
 static_assert(Tune<1>::step == 16 || Tune<1>::step == 32, "fp8 step must be 16 or 32");
 constexpr bool kLdsDma = PA_LDS_DMA != 0;
+constexpr bool kStageSwizzle = PA_STAGE_SWIZZLE != 0;
 
 // LDS-destination load of 16 bytes per lane: lane i's bytes land at dst + 16 i
 // (AUX: the cache-policy operand, 2 = non-temporal).
@@ -353,6 +361,8 @@ __device__ __forceinline__ void decode_split_body(const pa_decode_params& p, int
     constexpr int  CPR   = ROW / 16;                // 16-byte chunks per row
     constexpr int  HCH   = 16 * CPR;                // 16-byte chunks per half (256 B per row x 16)
     constexpr bool DMA   = STG && kLdsDma;          // the stage is filled by LDS-destination loads
+    // The stage's chunk permutation of row r (XOR with r % CPR).
+    auto swz = [](int r) { return kStageSwizzle ? r % CPR : 0; };
     static_assert(!DMA || DEPTH == 1, "the LDS-destination stage holds one step");
     using VRaw = std::conditional_t<EB == 2, u32x4, u32x2>;
     using KRaw = std::conditional_t<KL == 16, u32x4, u32x2>;
@@ -403,7 +413,7 @@ __device__ __forceinline__ void decode_split_body(const pa_decode_params& p, int
     int dma_chunk[NPART];
 #pragma unroll
     for (int part = 0; part < NPART; ++part)
-        dma_chunk[part] = 16 * ((lane % CPR) ^ ((RPP * part + lane / CPR) % CPR));
+        dma_chunk[part] = 16 * ((lane % CPR) ^ swz(RPP * part + lane / CPR));
     u32x4* const stage = stage_lds[STG ? wave : 0];
 
     // ---- pipeline registers, indexed by ring slot = step index mod DEPTH
@@ -760,7 +770,7 @@ __device__ __forceinline__ void decode_split_body(const pa_decode_params& p, int
 #pragma unroll
                     for (int part = 0; part < NPART; ++part) {
                         const int row  = RPP * part + wrow;
-                        const int slot = CPR * row + ((lane % CPR) ^ (row % CPR));
+                        const int slot = CPR * row + ((lane % CPR) ^ swz(row));
                         st[hh * HCH + slot]        = kc[s][hh][part];
                         st[(NH + hh) * HCH + slot] = vc[s][hh][part];
                     }
@@ -771,16 +781,16 @@ __device__ __forceinline__ void decode_split_body(const pa_decode_params& p, int
 #pragma unroll
                 for (int u = 0; u < NK; ++u) {
                     const int ch = (kb * KLANE + KSTEP * u) / 16;   // chunk of row c this load holds
-                    kr[s][hh][u] = st[hh * HCH + CPR * c + (ch ^ (c % CPR))];
+                    kr[s][hh][u] = st[hh * HCH + CPR * c + (ch ^ swz(c))];
                 }
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const int row = 4 * kb + r;
                     const u32x4* vrow = st + (NH + hh) * HCH + CPR * row;
                     if constexpr (EB == 2) {
-                        vr[s][hh][r] = vrow[c ^ (row % CPR)];
+                        vr[s][hh][r] = vrow[c ^ swz(row)];
                     } else {
-                        vr[s][hh][r] = reinterpret_cast<const u32x2*>(vrow)[2 * ((c >> 1) ^ (row % CPR)) + (c & 1)];
+                        vr[s][hh][r] = reinterpret_cast<const u32x2*>(vrow)[2 * ((c >> 1) ^ swz(row)) + (c & 1)];
                     }
                 }
             }
