@@ -77,11 +77,20 @@ typedef struct pa_decode_params {
     float*          partial_lse;       /* [num_segments][group] */
     int32_t         max_item_segments; /* most segments of one (row, kv head); sizes the
                                           merge launch (0 = unknown). Set by bind. */
-    int32_t         block_merge;       /* 1: every split (row, kv head) lies in one block of
-                                          8 work units and the split kernel merges it
-                                          (needs_merge is then 0). Set by bind. */
+    int32_t         block_merge;       /* How the split kernel merges split (row, kv head)
+                                          items itself (needs_merge is then 0). Set by bind.
+                                          0: it does not (the merge kernel does, if
+                                          needs_merge). 1: every split item lies in one
+                                          block of 8 work units and is merged there in LDS.
+                                          2: items spanning blocks are also merged in the
+                                          split kernel: each block writes one partial per
+                                          such item to the workspace, and the last block
+                                          to finish (merge_counters) combines them. */
     int32_t         num_segments;      /* segments of the bound plan (0 = unknown); sizes the
                                           partial workspace. Set by bind. */
+    int32_t*        merge_counters;    /* block_merge 2: one arrival counter per item, zero
+                                          between decodes (the plan zeroes them at upload;
+                                          every decode leaves them at zero). Set by bind. */
 } pa_decode_params;
 
 /* Thread-local message describing the last failed call ("" if none). */
@@ -126,6 +135,11 @@ int       pa_plan_num_ctas(const pa_plan* plan);
 int       pa_plan_tile(const pa_plan* plan);
 int       pa_plan_num_segments(const pa_plan* plan);
 int       pa_plan_num_items(const pa_plan* plan);
+/* How the split kernel merges this plan's split items, as DevicePlan::bind
+ * sets pa_decode_params.block_merge (0, 1 or 2; see there). No counterpart in
+ * the reference, whose plans always merge in a second kernel
+ * (decode.cu:143 needs_merge). Pure host. */
+pa_status pa_plan_merge_mode(const pa_plan* plan, int* out);
 /* Copies segments ([n][4]), cta_seg_begin ([num_ctas+1]) and item_seg_begin
  * ([items+1]); any output may be NULL. */
 pa_status pa_plan_copy(const pa_plan* plan, int32_t* segments, int32_t* cta_seg_begin,

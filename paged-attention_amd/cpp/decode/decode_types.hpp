@@ -54,6 +54,7 @@ struct DecodeParams {
     int max_item_segments = 0;    // most segments of one (row, head); sizes the merge (0 = unknown)
     int block_merge       = 0;    // split rows merged inside the split kernel (set by DevicePlan::bind)
     int num_segments      = 0;    // segments of the bound plan (set by DevicePlan::bind; 0 = unknown)
+    int* merge_counters   = nullptr;   // per-item arrival counters of block_merge 2 (set by DevicePlan::bind)
 };
 
 static_assert(sizeof(DecodeParams) == sizeof(pa_decode_params), "DecodeParams must match pa_decode_params");
@@ -64,6 +65,7 @@ static_assert(offsetof(DecodeParams, partial_lse) == offsetof(pa_decode_params, 
 static_assert(offsetof(DecodeParams, max_item_segments) == offsetof(pa_decode_params, max_item_segments));
 static_assert(offsetof(DecodeParams, block_merge) == offsetof(pa_decode_params, block_merge));
 static_assert(offsetof(DecodeParams, num_segments) == offsetof(pa_decode_params, num_segments));
+static_assert(offsetof(DecodeParams, merge_counters) == offsetof(pa_decode_params, merge_counters));
 static_assert(sizeof(int4) == 4 * sizeof(int32_t), "segments are int32 quadruples");
 
 namespace detail {

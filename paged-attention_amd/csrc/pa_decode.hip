@@ -53,13 +53,18 @@
 //     the segment's first K/V loads and expanded to the B-operand layout
 //     through a per-wave LDS slot once per segment; on the LDS-stage paths it
 //     lands there with the same LDS-destination loads, ahead of the K / V.
-//   * When every split row lies inside one block of 8 work units (e.g. 32
-//     rows x 8 kv heads x 8192 tokens over 2048 units) the rows are merged in
-//     the block and no merge launch is needed: a unit's split segments are
-//     only its first and last, so each wave keeps at most two partials (and
-//     their LSEs) in LDS; after one barrier every thread of the block merges
-//     one head-dim element of each split row into the output. Otherwise the
-//     partials go to the plan's HBM workspace for the merge kernel.
+//   * Split rows are merged by the split kernel itself when the plan allows
+//     (block_merge 1 and 2): a unit's split segments are only its first and
+//     last, so each wave keeps at most two partials (and their LSEs) in LDS;
+//     after one barrier every thread of the block merges one head-dim element
+//     of each split row. A row inside the block (e.g. 32 rows x 8 kv heads x
+//     8192 tokens over 2048 units) is then complete; a row that spans blocks
+//     (up to 16) leaves one device-coherent partial per block, and the last
+//     of its blocks to arrive (a per-row counter) combines them, in block
+//     order. No merge launch is needed. Otherwise (rows over more blocks, or
+//     caller plans that do not keep a row's segments in consecutive units)
+//     every split segment's partial goes to the plan's workspace for the
+//     merge kernel.
 
 #include "pa_device.hpp"
 
@@ -135,6 +140,25 @@
 #define PA_LDS_DMA 1
 #endif
 
+// Diagnostic builds only (PA_STAMPS=1): per-block s_memrealtime stamps of the
+// split kernel's phases, read back with pa_debug_stamps.
+#ifndef PA_STAMPS
+#define PA_STAMPS 0
+#endif
+#if PA_STAMPS
+__device__ unsigned long long pa_stamps[4096 * 16];
+extern "C" int pa_debug_stamps(void* host, unsigned long bytes) {
+    return static_cast<int>(hipMemcpyFromSymbol(host, HIP_SYMBOL(pa_stamps), bytes, 0, hipMemcpyDeviceToHost));
+}
+#endif
+__device__ __forceinline__ void stamp(int k) {
+#if PA_STAMPS
+    if ((threadIdx.x & 63) == 0 && blockIdx.x < 4096) pa_stamps[blockIdx.x * 16 + k] = __builtin_amdgcn_s_memrealtime();
+#else
+    (void)k;
+#endif
+}
+
 namespace pa {
 namespace {
 
@@ -143,6 +167,9 @@ constexpr float kRescaleSlack = 8.0f;   // log2 headroom of the lazy running max
 constexpr float kLog2e        = 1.4426950408889634f;
 // The cache-policy operand of buffer loads (2 = non-temporal).
 template <bool NT> constexpr int kAux = NT ? 2 : 0;
+// ... and of a device-coherent load (sc1: served from the device's coherence
+// point, like a relaxed agent-scope atomic load).
+constexpr int kAuxCoherent = 16;
 
 template <int EB> struct Tune {
     static constexpr int  step  = EB == 2 ? PA_FP16_STEP : PA_FP8_STEP;
@@ -263,30 +290,53 @@ __device__ __forceinline__ float dpp_f32(float x) {
     return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(v, v, CTRL, 0xF, 0xF, false));
 }
 
+// Device-coherent store of the partials that blocks exchange inside one launch:
+// a relaxed agent-scope atomic store, written through to the device's
+// coherence point (the XCDs' L2 caches are not coherent with each other), and
+// complete there once the wave's vector memory counter has drained. The
+// reads use the same scope's cache policy (kAuxCoherent).
+__device__ __forceinline__ void store_coherent(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Block-level merge after the split loop. slot_item holds, per wave, the
 // (row, kv head) item of its first (slot 0) and last (slot 1) segment when that
-// segment is a split one, else -1; part / lse hold the slot's normalized
-// partial rows and base-2 LSEs, written to LDS by the wave that computed them.
-// The planner turns this merge on only when every split row lies in one block,
-// so the slots holding one item are that row's whole set of partials. Each
-// thread owns one head-dim element (two for G = 8) of every item and reads
-// that element of all 16 slots at once, with the LSEs and slot items (one LDS
-// round trip). An item's weights 2^(lse - max) depend only on the slot and the
-// head, and a wave's 64 elements share one head, so lane j of each wave
-// computes slot j's weight once (0 outside the item) and the element sums take
-// them as wave-uniform operands: per item, the base-2 LSE-weighted average of
-// its partials (decode_kernels.cuh:409-432), summed in slot order, written as
-// fp16. No branch depends on a slot.
+// segment is a split one, else -1 (slot_seg: that segment's index); part / lse
+// hold the slot's normalized partial rows and base-2 LSEs, written to LDS by
+// the wave that computed them. Each thread owns one head-dim element (two for
+// G = 8) of every item and reads that element of all 16 slots at once, with
+// the LSEs and slot items (one LDS round trip). An item's weights
+// 2^(lse - max) depend only on the slot and the head, and a wave's 64
+// elements share one head, so lane j of each wave computes slot j's weight
+// once (0 outside the item) and the element sums take them as wave-uniform
+// operands: the base-2 LSE-weighted average of the item's partials in this
+// block (decode_kernels.cuh:409-432), summed in slot order. No branch depends
+// on a slot.
+//
+// An item whose segments all lie in this block (block_merge 1: every split
+// item) is written as fp16. With block_merge 2 an item may also span blocks
+// (its k-th segment runs in unit u0 + k, so it continues from the previous
+// block at the block's first slot and into the next at its last): the block's
+// average becomes one partial row of the item, at the workspace slot of the
+// item's first segment in the block, with LSE max + log2(sum of weights).
+// After every thread's stores are complete, one lane per such item adds one to
+// the item's counter; the block that brings it to the item's block count
+// resets it to zero and combines the item's block partials, in block order, as
+// the merge kernel does (so the result does not depend on which block is
+// last). Blocks never wait for each other.
 template <int G>
-__device__ __forceinline__ void block_merge(const pa_decode_params& p, const int (*slot_item)[2],
-                                            const float (*part)[G * kHeadDim], const float (*lse)[G], int tid) {
+__device__ __forceinline__ void block_merge(const pa_decode_params& p, const int32_t* __restrict__ isb,
+                                            const int (*slot_item)[2], const int (*slot_seg)[2],
+                                            const float (*part)[G * kHeadDim], const float (*lse)[G],
+                                            int* last_lds, int tid, int lblock) {
     constexpr int NS = 2 * kWaves;
     constexpr int NO = G * kHeadDim;
     constexpr int NE = (NO + 64 * kWaves - 1) / (64 * kWaves);   // elements per thread
     static_assert(NS == 16, "the slot lanes form one DPP row");
     static_assert(kHeadDim % 64 == 0, "a wave's elements share one head");
-    const int  lane = tid & 63;
-    const bool slot = lane < NS;   // lane j holds slot j
+    const int  lane  = tid & 63;
+    const bool slot  = lane < NS;   // lane j holds slot j
+    const bool chain = p.block_merge == 2;
     float lv[NE], pv[NE][NS];
 #pragma unroll
     for (int e = 0; e < NE; ++e) {
@@ -298,16 +348,29 @@ __device__ __forceinline__ void block_merge(const pa_decode_params& p, const int
         }
     }
     const int      mine   = slot_item[(lane & (NS - 1)) >> 1][lane & 1];
+    const int      myseg  = slot_seg[(lane & (NS - 1)) >> 1][lane & 1];
     const uint64_t filled = __builtin_amdgcn_ballot_w64(slot && mine >= 0);
+    // Items of this block that span blocks (at most two), block-uniform.
+    int ns = 0, sx0 = 0, su0 = 0, sn0 = 0, sx1 = 0, su1 = 0, sn1 = 0;
+    uint64_t run = 0;
+    for (uint64_t rem = filled; rem != 0; rem &= ~run) {
+        const int j0 = __builtin_ctzll(rem);
+        const int x  = __builtin_amdgcn_readlane(mine, j0);   // the next item
+        run = __builtin_amdgcn_ballot_w64(slot && mine == x);
+        const int  n     = isb[x + 1] - isb[x];
+        const bool spans = chain && __builtin_popcountll(run) != n;
+        const int  bseg  = __builtin_amdgcn_readlane(myseg, j0);   // the item's first segment here
+        if (spans) {
+            const int u0 = lblock * kWaves + (j0 >> 1) - (bseg - isb[x]);   // unit of its first segment
+            if (ns == 0) { sx0 = x; su0 = u0; sn0 = n; }
+            else { sx1 = x; su1 = u0; sn1 = n; }
+            ++ns;
+        }
+        const bool in = (run >> lane) & 1;
 #pragma unroll
-    for (int e = 0; e < NE; ++e) {
-        const int o = tid + 64 * kWaves * e;
-        if (o >= NO) break;
-        uint64_t run = 0;
-        for (uint64_t rem = filled; rem != 0; rem &= ~run) {
-            const int x = __builtin_amdgcn_readlane(mine, __builtin_ctzll(rem));   // the next item
-            run = __builtin_amdgcn_ballot_w64(slot && mine == x);
-            const bool in = (run >> lane) & 1;
+        for (int e = 0; e < NE; ++e) {
+            const int o = tid + 64 * kWaves * e;
+            if (o >= NO) break;
             // The item's maximum LSE over the 16 slot lanes (one DPP row):
             // swaps of neighbours and pairs in each quad, then rotations by 4
             // and 8.
@@ -324,10 +387,137 @@ __device__ __forceinline__ void block_merge(const pa_decode_params& p, const int
                 a   = fmaf(wj, ((run >> j) & 1) ? pv[e][j] : 0.f, a);   // empty slots hold no partial
                 den = den + wj;
             }
-            const int b = x / p.num_kv_heads, h = x - b * p.num_kv_heads;
-            p.out[(static_cast<size_t>(b) * p.num_q_heads + h * G) * kHeadDim + o] =
-                __builtin_bit_cast(uint16_t, static_cast<_Float16>(a * (1.0f / den)));
+            if (!spans) {
+                const int b = x / p.num_kv_heads, h = x - b * p.num_kv_heads;
+                p.out[(static_cast<size_t>(b) * p.num_q_heads + h * G) * kHeadDim + o] =
+                    __builtin_bit_cast(uint16_t, static_cast<_Float16>(a * (1.0f / den)));
+            } else {
+                store_coherent(p.partial_out + static_cast<size_t>(bseg) * NO + o, a * (1.0f / den));
+                if (o % kHeadDim == 0)
+                    store_coherent(p.partial_lse + static_cast<size_t>(bseg) * G + o / kHeadDim, mx + __log2f(den));
+            }
         }
+    }
+    if (ns == 0) return;
+    if (tid == 0) stamp(9);
+
+    // Arrivals: this block's partial rows are complete at the coherence point
+    // before its counters move.
+    __builtin_amdgcn_s_waitcnt(kWaitVm0);
+    __syncthreads();
+    if (tid == 0) stamp(10);
+    if (tid < ns) {
+        const int x  = tid == 0 ? sx0 : sx1;
+        const int u0 = tid == 0 ? su0 : su1;
+        const int n  = tid == 0 ? sn0 : sn1;
+        const int nb = (u0 + n - 1) / kWaves - u0 / kWaves + 1;   // blocks the item spans
+        int* ctr = p.merge_counters + x;
+        const int before = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const bool last = before == nb - 1;
+        if (last) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);   // for the next decode
+        last_lds[tid] = last;
+    }
+    __syncthreads();
+    if (tid == 0) stamp(11);
+    // The last block combines the item's block partials (block j's sits at the
+    // item's first segment in block j). Thread (v, g), g = tid % NGR, takes
+    // 16 bytes (4 dims) v of every NGR-th block from g on, up to 8 blocks at a
+    // time, each with one coherent 16-byte load of the row and one of its LSE,
+    // all issued before the first is used (one round trip), and keeps a
+    // running maximum over them in block order; the NGR states of one dim
+    // vector sit in adjacent lanes of one DPP row and are combined in a fixed
+    // tree (lanes 1, 2 apart, then quad and half-row mirrors), so the result
+    // does not depend on timing.
+    constexpr int NV  = NO / 4;                  // 16-byte vectors of one block partial
+    constexpr int NGR = 64 * kWaves / NV;        // lanes sharing one vector (16, 8, 4, 2 for G = 1, 2, 4, 8)
+    static_assert(NGR >= 1 && NGR <= 16 && (NGR & (NGR - 1)) == 0, "the groups of a vector form one DPP row");
+    const int gi = tid % NGR;
+    const int vi = tid / NGR;
+    const int hh = 4 * vi / kHeadDim;            // query head of the vector
+    for (int i = 0; i < ns; ++i) {
+        if (!last_lds[i]) continue;
+        const int x  = i == 0 ? sx0 : sx1;
+        const int u0 = i == 0 ? su0 : su1;
+        const int n  = i == 0 ? sn0 : sn1;
+        const int s0 = isb[x];
+        const int j0 = u0 / kWaves, j1 = (u0 + n - 1) / kWaves;
+        const int nb = j1 - j0 + 1;
+        const int b = x / p.num_kv_heads, h = x - b * p.num_kv_heads;
+        // The item's partial rows and LSEs, from its first segment on (byte
+        // offsets fit 32 bits: n segments of NO floats).
+        const __amdgpu_buffer_rsrc_t rs =
+            buffer_rsrc(p.partial_out + static_cast<size_t>(s0) * NO, n * NO * static_cast<int>(sizeof(float)));
+        const __amdgpu_buffer_rsrc_t rl =
+            buffer_rsrc(p.partial_lse + static_cast<size_t>(s0) * G, n * G * static_cast<int>(sizeof(float)));
+        float  m = -INFINITY, den = 0.f;
+        f32x4  acc = {0.f, 0.f, 0.f, 0.f};
+        const int per = (nb + NGR - 1) / NGR;   // blocks per group (the first groups may take one more)
+        for (int k0 = 0; k0 < per; k0 += 8) {
+            u32x4 raw[8];
+            float ls[8];
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                const int j = j0 + gi + NGR * (k0 + t);
+                if (j <= j1) {
+                    const int k = max(0, kWaves * j - u0);   // the block's first segment, from s0
+                    raw[t] = __builtin_bit_cast(
+                        u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                   rs, (k * NO + 4 * vi) * static_cast<int>(sizeof(float)), 0, kAuxCoherent));
+                    ls[t] = __builtin_bit_cast(
+                        float, __builtin_amdgcn_raw_buffer_load_b32(
+                                   rl, (k * G + hh) * static_cast<int>(sizeof(float)), 0, kAuxCoherent));
+                }
+            }
+#if PA_STAMPS
+            __builtin_amdgcn_s_waitcnt(kWaitVm0);
+            if (tid == 0 && i == 0 && k0 == 0) stamp(12);
+#endif
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                const int j = j0 + gi + NGR * (k0 + t);
+                if (j > j1) break;
+                const float mn  = fmaxf(m, ls[t]);
+                const float f   = exp2_fast(m - mn);   // 0 while m = -inf
+                const float wgt = exp2_fast(ls[t] - mn);
+                const f32x4 v   = __builtin_bit_cast(f32x4, raw[t]);
+#pragma unroll
+                for (int c = 0; c < 4; ++c) acc[c] = fmaf(wgt, v[c], acc[c] * f);
+                den = fmaf(den, f, wgt);
+                m   = mn;
+            }
+        }
+        // Combine the NGR states of the vector (a group with no block has
+        // m = -inf and weighs 0).
+        auto combine = [&](float m2, float d2, const f32x4& a2) {
+            const float mt = fmaxf(m, m2);
+            const float f1 = m == -INFINITY ? 0.f : exp2_fast(m - mt);
+            const float f2 = m2 == -INFINITY ? 0.f : exp2_fast(m2 - mt);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) acc[c] = acc[c] * f1 + a2[c] * f2;
+            den = den * f1 + d2 * f2;
+            m   = mt;
+        };
+        auto partner_round = [&](auto ctrl) {
+            constexpr int C = decltype(ctrl)::value;
+            f32x4 a2;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) a2[c] = dpp_f32<C>(acc[c]);
+            combine(dpp_f32<C>(m), dpp_f32<C>(den), a2);
+        };
+        if (tid == 0 && i == 0) stamp(13);
+        if constexpr (NGR >= 2) partner_round(std::integral_constant<int, 0xB1>{});    // quad_perm [1,0,3,2]
+        if constexpr (NGR >= 4) partner_round(std::integral_constant<int, 0x4E>{});    // quad_perm [2,3,0,1]
+        if constexpr (NGR >= 8) partner_round(std::integral_constant<int, 0x141>{});   // row_half_mirror
+        if constexpr (NGR >= 16) partner_round(std::integral_constant<int, 0x140>{});  // row_mirror
+        if (tid == 0 && i == 0) stamp(14);
+        if (gi == 0) {
+            const float inv = 1.0f / den;
+            const f16x2 lo = {static_cast<_Float16>(acc[0] * inv), static_cast<_Float16>(acc[1] * inv)};
+            const f16x2 hi = {static_cast<_Float16>(acc[2] * inv), static_cast<_Float16>(acc[3] * inv)};
+            *reinterpret_cast<u32x2*>(p.out + (static_cast<size_t>(b) * p.num_q_heads + h * G) * kHeadDim + 4 * vi) =
+                u32x2{__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi)};
+        }
+        if (tid == 0 && i == 0) stamp(15);
     }
 }
 
@@ -371,6 +561,8 @@ __device__ __forceinline__ void decode_split_body(const pa_decode_params& p, int
     // by issue() with the K / V, 1 KiB per load).
     __shared__ __attribute__((aligned(16))) u32x4 q_lds[kWaves][64 * NQ];
     __shared__ int slot_item[kWaves][2];                                     // split segments per wave
+    __shared__ int slot_seg[kWaves][2];                                      // their segment indices
+    __shared__ int last_lds[2];                                              // block merges a spanning item
     // LDS stage of one step per wave (STG): [K, V][half][16 rows][row bytes],
     // each row's 16-byte chunks XOR-swizzled by (row % chunks per row).
     __shared__ __attribute__((aligned(16))) u32x4 stage_lds[STG ? kWaves : 1][STG ? 2 * NH * HCH : 1];
@@ -378,9 +570,11 @@ __device__ __forceinline__ void decode_split_body(const pa_decode_params& p, int
     __shared__ __attribute__((aligned(16))) float part_lds[2 * kWaves][G * kHeadDim];
     __shared__ float lse_lds[2 * kWaves][G];
 
+    if (threadIdx.x == 0) stamp(0);
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int unit = blockIdx.x * kWaves + wave;
+    const int lblock = static_cast<int>(blockIdx.x);   // units 8 lblock .. 8 lblock + 7
+    const int unit   = lblock * kWaves + wave;
     const bool merge_here = p.block_merge != 0;   // block-level merge of split rows
     if (lane == 0) {
         slot_item[wave][0] = -1;
@@ -705,7 +899,10 @@ __device__ __forceinline__ void decode_split_body(const pa_decode_params& p, int
                         if (c == 0) p.partial_lse[static_cast<size_t>(C.seg) * G + 4 * kb + i] = ls;
                     }
                 }
-                if (merge_here && lane == 0) slot_item[wave][sl] = C.b * hkv + C.h;
+                if (merge_here && lane == 0) {
+                    slot_item[wave][sl] = C.b * hkv + C.h;
+                    slot_seg[wave][sl]  = C.seg;
+                }
             }
         }
         m_run = -INFINITY;
@@ -959,10 +1156,11 @@ __device__ __forceinline__ void decode_split_body(const pa_decode_params& p, int
         if constexpr (DEPTH > 3) if (!advance(3)) break;
     }
     }   // seg_begin < seg_end
+    stamp(1 + wave);
 
     if (merge_here) {
         __syncthreads();
-        block_merge<G>(p, slot_item, part_lds, lse_lds, threadIdx.x);
+        block_merge<G>(p, isb, slot_item, slot_seg, part_lds, lse_lds, last_lds, threadIdx.x, lblock);
     }
 }
 
@@ -1257,6 +1455,9 @@ hipError_t launch_decode_split(int dtype, const pa_decode_params& p, hipStream_t
         throw std::invalid_argument("decode: null pointer in params");
     if ((p.needs_merge || p.block_merge) && (!p.partial_out || !p.partial_lse))
         throw std::invalid_argument("decode: split rows need the partial workspace");
+    if (p.block_merge < 0 || p.block_merge > 2) throw std::invalid_argument("decode: block_merge must be 0, 1 or 2");
+    if (p.block_merge == 2 && !p.merge_counters)
+        throw std::invalid_argument("decode: block_merge 2 needs the plan's merge counters");
     return dtype == PA_KV_FP16 ? launch_split_e<2>(p, g, s) : launch_split_e<1>(p, g, s);
 }
 

@@ -62,7 +62,8 @@ struct pa_device_plan {
     int      needs_merge = 0;
     int      max_item_segments = 0;
     int      num_segments = 0;
-    bool     block_merge = false;
+    int      block_merge = 0;          // pa_decode_params.block_merge of the plan
+    int32_t* merge_counters = nullptr;  // per-item counters in `ints`
     pa_stage_pool staging;
 };
 
@@ -136,6 +137,9 @@ void free_stages(pa_stage_pool& sp);
 
 // ---- planner and device plan (pa_plan.cpp)
 void check_dtype(int dtype);
+// pa_decode_params.block_merge for a plan: 0 (merge kernel), 1 (every split
+// item inside one block), 2 (items spanning blocks merged by the split kernel).
+int  plan_merge_mode(const pa_plan& plan);
 void make_plan_impl(pa_plan& plan, int dtype, const int32_t* lens, int batch, int hq, int hkv, int hd,
                     int num_ctas);
 // Queues the plan's arrays (and n_extra caller ints, kept at dp.extra) for the

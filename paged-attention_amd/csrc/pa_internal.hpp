@@ -30,6 +30,11 @@ constexpr int kGroupTokens = 16;    // tokens per MFMA step of the decode kernel
 #define PA_BLOCK_UNITS 8
 #endif
 constexpr int kBlockUnits  = PA_BLOCK_UNITS;   // work units (waves) per block of the decode kernel
+// 1: plans whose split (row, kv head) items span blocks are merged inside the
+// split kernel (pa_decode_params.block_merge 2); 0: by the merge kernel.
+#ifndef PA_CHAIN_MERGE
+#define PA_CHAIN_MERGE 1
+#endif
 
 // Byte gap between the end of the K pool and the start of the V pool when both
 // share one allocation. A wave reads the same (page, kv head) run of K and of

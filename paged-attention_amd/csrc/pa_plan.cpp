@@ -105,6 +105,44 @@ void check_dtype(int dtype) {
     if (dtype != PA_KV_FP16 && dtype != PA_KV_FP8_E4M3)
         throw std::invalid_argument("unknown kv dtype " + std::to_string(dtype));
 }
+constexpr int kChainMaxBlocks = 16;   // blocks one item may span under block_merge 2
+int plan_merge_mode(const pa_plan& plan) {
+    const size_t nseg = plan.segments.size() / 4;
+    if (nseg <= static_cast<size_t>(plan.items)) return 0;   // no split items
+    // The split kernel keeps a unit's split segments in two LDS slots: they
+    // must be the unit's first and last segments (true of every make_plan cut).
+    std::vector<int32_t> unit_of(nseg, 0);
+    for (int u = 0; u < plan.num_ctas; ++u)
+        for (int sg = plan.cta_seg_begin[u]; sg < plan.cta_seg_begin[u + 1]; ++sg)
+            unit_of[static_cast<size_t>(sg)] = u;
+    bool in_block = true, consecutive = true;
+    for (int i = 0; i < plan.items; ++i) {
+        const int a = plan.item_seg_begin[i], z = plan.item_seg_begin[i + 1];
+        if (z - a <= 1) continue;
+        const int u0 = unit_of[static_cast<size_t>(a)];
+        const int nb = unit_of[static_cast<size_t>(z - 1)] / pa::kBlockUnits - u0 / pa::kBlockUnits + 1;
+        if (nb > 1) in_block = false;
+        // The split kernel's combine of a spanning item runs on one CU and
+        // reads one partial per block: past 16 blocks per item the merge
+        // kernel, which spreads every item over many CUs, is faster (one
+        // MI355X, fp16 and FP8: 16 blocks per item 1.0-1.3 us faster in the
+        // split kernel, 32 blocks 0.5-2.7 us slower). It addresses the
+        // partial rows with 32-bit offsets (segments x 8 heads x 128 floats).
+        if (nb > kChainMaxBlocks || z - a >= (1 << 19)) consecutive = false;
+        for (int sg = a; sg < z; ++sg) {
+            const int u = unit_of[static_cast<size_t>(sg)];
+            if (sg != plan.cta_seg_begin[u] && sg != plan.cta_seg_begin[u + 1] - 1) return 0;
+            if (u != u0 + (sg - a)) consecutive = false;
+        }
+    }
+    if (in_block) return 1;
+    // Chained merge: a block finds an item's other blocks from the unit of the
+    // item's first segment, which needs the item's k-th segment in unit u0 + k.
+#if PA_CHAIN_MERGE
+    if (consecutive) return 2;
+#endif
+    return 0;
+}
 void make_plan_impl(pa_plan& plan, int dtype, const int32_t* lens, int batch, int hq, int hkv, int hd,
                     int num_ctas) {
     const int group = group_of(hq, hkv);
@@ -169,13 +207,15 @@ void device_plan_upload(pa_device_plan& dp, const pa_plan& plan, int group, int 
     for (size_t i = 0; i < nseg; ++i)
         if (plan.segments[4 * i + 2] % pa::kGroupTokens != 0)
             throw std::invalid_argument("upload: segment starts must be multiples of 16 tokens");
-    // One block: segments | cta_seg_begin | item_seg_begin | extra, each part
-    // starting on a 16-byte boundary (the kernels read segments as int4).
+    // One block: segments | cta_seg_begin | item_seg_begin | extra | merge
+    // counters, each part starting on a 16-byte boundary (the kernels read
+    // segments as int4).
     auto round4 = [](size_t n) { return (n + 3) & ~size_t{3}; };
     const size_t o_cta   = round4(plan.segments.size());
     const size_t o_item  = o_cta + round4(plan.cta_seg_begin.size());
     const size_t o_extra = o_item + round4(plan.item_seg_begin.size());
-    const size_t total   = o_extra + round4(n_extra);
+    const size_t o_ctr   = o_extra + round4(n_extra);   // per-item merge counters, uploaded as zeros
+    const size_t total   = o_ctr + round4(static_cast<size_t>(plan.items));
     if (total > dp.ints_cap) {
         // Growing frees the old block, which decodes queued before may still
         // read: wait for them first (growth only happens for a plan larger
@@ -193,6 +233,7 @@ void device_plan_upload(pa_device_plan& dp, const pa_plan& plan, int group, int 
     std::copy(plan.cta_seg_begin.begin(), plan.cta_seg_begin.end(), st.host + o_cta);
     std::copy(plan.item_seg_begin.begin(), plan.item_seg_begin.end(), st.host + o_item);
     if (n_extra) std::copy(extra, extra + n_extra, st.host + o_extra);
+    std::fill(st.host + o_ctr, st.host + total, 0);
     pa::hip_check(hipMemcpyAsync(dp.ints, st.host, total * sizeof(int32_t), hipMemcpyHostToDevice, s),
                   "hipMemcpyAsync plan");
     release_stage(st, s);
@@ -200,6 +241,7 @@ void device_plan_upload(pa_device_plan& dp, const pa_plan& plan, int group, int 
     dp.cta_seg_begin  = dp.ints + o_cta;
     dp.item_seg_begin = dp.ints + o_item;
     dp.extra          = n_extra ? dp.ints + o_extra : nullptr;
+    dp.merge_counters = dp.ints + o_ctr;
     const size_t rows = nseg * static_cast<size_t>(group);
     const size_t need = rows * (static_cast<size_t>(head_dim) + 1);
     if (need > dp.part_cap) {
@@ -212,30 +254,8 @@ void device_plan_upload(pa_device_plan& dp, const pa_plan& plan, int group, int 
     dp.partial_lse = dp.partial_out ? dp.partial_out + rows * head_dim : nullptr;
     dp.num_ctas = plan.num_ctas;
     dp.num_segments = static_cast<int>(nseg);
-    // Block-level merge: the split kernel merges a split row itself when all
-    // its segments lie in one block of kBlockUnits units. It needs every split
-    // segment to be its unit's first or last (true of every make_plan cut) and
-    // is used when it covers every split row, so no merge launch remains.
-    bool block_merge = nseg > static_cast<size_t>(plan.items);
-    if (block_merge) {
-        std::vector<int32_t> unit_of(nseg, 0);
-        for (int u = 0; u < plan.num_ctas; ++u)
-            for (int sg = plan.cta_seg_begin[u]; sg < plan.cta_seg_begin[u + 1]; ++sg)
-                unit_of[static_cast<size_t>(sg)] = u;
-        for (int i = 0; i < plan.items && block_merge; ++i) {
-            const int a = plan.item_seg_begin[i], z = plan.item_seg_begin[i + 1];
-            if (z - a <= 1) continue;
-            if (unit_of[static_cast<size_t>(a)] / pa::kBlockUnits != unit_of[static_cast<size_t>(z - 1)] / pa::kBlockUnits)
-                block_merge = false;   // the row spans blocks
-            for (int sg = a; sg < z && block_merge; ++sg) {
-                const int u = unit_of[static_cast<size_t>(sg)];
-                if (sg != plan.cta_seg_begin[u] && sg != plan.cta_seg_begin[u + 1] - 1)
-                    block_merge = false;   // a split segment inside a unit
-            }
-        }
-    }
-    dp.block_merge = block_merge;
-    dp.needs_merge = !block_merge && nseg > static_cast<size_t>(plan.items) ? 1 : 0;
+    dp.block_merge = plan_merge_mode(plan);
+    dp.needs_merge = dp.block_merge == 0 && nseg > static_cast<size_t>(plan.items) ? 1 : 0;
     dp.max_item_segments = 0;
     for (int i = 0; i < plan.items; ++i)
         dp.max_item_segments = std::max(dp.max_item_segments, plan.item_seg_begin[i + 1] - plan.item_seg_begin[i]);
@@ -249,8 +269,9 @@ void device_plan_bind(const pa_device_plan& dp, pa_decode_params& p) {
     p.partial_out    = dp.partial_out;
     p.partial_lse    = dp.partial_lse;
     p.max_item_segments = dp.max_item_segments;
-    p.block_merge       = dp.block_merge ? 1 : 0;
+    p.block_merge       = dp.block_merge;
     p.num_segments      = dp.num_segments;
+    p.merge_counters    = dp.merge_counters;
 }
 void device_plan_free(pa_device_plan& dp) {
     free_stages(dp.staging);
@@ -376,6 +397,12 @@ int  pa_plan_num_ctas(const pa_plan* plan) { return plan ? plan->num_ctas : 0; }
 int  pa_plan_tile(const pa_plan* plan) { return plan ? plan->tile : 0; }
 int  pa_plan_num_segments(const pa_plan* plan) { return plan ? static_cast<int>(plan->segments.size() / 4) : 0; }
 int  pa_plan_num_items(const pa_plan* plan) { return plan ? plan->items : 0; }
+pa_status pa_plan_merge_mode(const pa_plan* plan, int* out) {
+    return guarded([&] {
+        if (!plan || !out) throw std::invalid_argument("plan or out is null");
+        *out = plan_merge_mode(*plan);
+    });
+}
 
 pa_status pa_plan_copy(const pa_plan* plan, int32_t* segments, int32_t* cta_seg_begin, int32_t* item_seg_begin) {
     return guarded([&] {

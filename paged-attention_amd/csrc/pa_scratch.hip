@@ -17,7 +17,7 @@
 // before anything is launched. Every call on one GPU shares that GPU's array:
 // calls that overlap on one GPU (two streams, two host threads) race on it.
 // Nothing in it needs to start at zero: the split kernel writes every partial
-// the merge kernel reads.
+// that is read back (the merge counters of block_merge 2 live in the plan).
 
 #include "pa_host.hpp"
 
@@ -90,11 +90,11 @@ pa_status pa_decode_static(int dtype, const pa_decode_params* p, int num_segment
             throw std::invalid_argument("decode_static: a plan with split rows needs needs_merge or block_merge");
         const size_t group = static_cast<size_t>(p->num_q_heads / p->num_kv_heads);
         const size_t rows  = static_cast<size_t>(p->num_segments) * group;
-        // Only plans merged by the merge kernel write partials to the
-        // workspace, rows * (head_dim + 1) floats; plans merged inside the
-        // split kernel keep theirs in LDS, and plans without split rows write
-        // none.
-        const bool   hbm_partials = split_rows && !p->block_merge;
+        // Plans merged by the merge kernel, or across blocks inside the split
+        // kernel (block_merge 2), write partials to the workspace, at most
+        // rows * (head_dim + 1) floats; plans merged inside one block keep
+        // theirs in LDS, and plans without split rows write none.
+        const bool   hbm_partials = split_rows && p->block_merge != 1;
         const size_t need = hbm_partials ? rows * (static_cast<size_t>(pa::kHeadDim) + 1) * sizeof(float) : 0;
         if (need > kScratchBytes)
             throw std::length_error("decode_static: the plan's partial workspace (" + std::to_string(need) +

@@ -74,6 +74,7 @@ class DecodeParams(ctypes.Structure):
         ("max_item_segments", ctypes.c_int32),
         ("block_merge", ctypes.c_int32),
         ("num_segments", ctypes.c_int32),
+        ("merge_counters", ctypes.c_void_p),
     ]
 
 
@@ -117,6 +118,7 @@ SIGNATURES: dict[str, tuple] = {
     "pa_plan_tile": (_I, [_P]),
     "pa_plan_num_segments": (_I, [_P]),
     "pa_plan_num_items": (_I, [_P]),
+    "pa_plan_merge_mode": (_I, [_P, _PI]),
     "pa_plan_copy": (_I, [_P, _P, _P, _P]),
     "pa_device_plan_create": (_I, [_PP]),
     "pa_device_plan_destroy": (None, [_P]),

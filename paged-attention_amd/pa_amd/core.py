@@ -130,6 +130,17 @@ class DecodePlan:
     def needs_merge(self) -> bool:
         return len(self.segments) > len(self.item_seg_begin) - 1
 
+    @property
+    def merge_mode(self) -> int:
+        """pa_decode_params.block_merge that DevicePlan.bind sets for this plan:
+        0 (merge kernel), 1 (split items merged inside one block), 2 (items
+        spanning blocks merged by the split kernel too)."""
+        if self.handle is None:
+            raise ValueError("plan has no native handle")
+        out = ctypes.c_int(0)
+        call("pa_plan_merge_mode", self.handle.value, ctypes.byref(out))
+        return out.value
+
 
 class _PlanHandle:
     def __init__(self, h: int):

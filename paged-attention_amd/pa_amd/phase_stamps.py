@@ -1,0 +1,118 @@
+"""Where a decode step's time goes inside the split kernel: per-block
+s_memrealtime stamps of its phases, from a diagnostic build of the library.
+
+    python3 build.py -D PA_STAMPS=1 --lib lib/variants/libpa_decode_stamps.so
+    PA_DECODE_LIB=lib/variants/libpa_decode_stamps.so \\
+        python3 -m pa_amd.phase_stamps [--shape B L fp16|fp8]... [--merge-kernel]
+
+For each shape (default: 4 x 1024, 2 x 16384 and 1 x 131072, fp16 and FP8 for
+the last) a populated cache (bench_decode.Setup: 16-token shuffled pages, the
+default grid) runs 50 warm decode steps, then 200 timed back to back (HIP
+events: the period of one step), and the stamps of the last step are read
+back. Times are microseconds after the first block started (100 MHz clock).
+One JSON line per shape:
+
+  period_us          one step back to back (kernel plus the gap to the next)
+  wave_end           p0 / p50 / p100 of the waves' ends of their split loop
+  merge_in_block     per block, from its last wave's end to its merged items
+                     (the LDS merge, and for items that span blocks the
+                     partial row stored)
+  store_wait         those partial rows complete at the coherence point
+  arrive             the arrival counter's round trip
+  combine            the last block's combine of an item's block partials:
+                     loads returned / running maximum / lane tree / output
+  last_end           the last stamp of the step
+
+The phases after `wave_end` exist when the plan merges across blocks inside
+the split kernel (block_merge 2); --merge-kernel forces the merge kernel on
+the same plan instead (block_merge 0), whose launch the period then includes.
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import sys
+
+from . import core
+from .bench_decode import Setup
+
+TICK_US = 0.01   # s_memrealtime runs at 100 MHz
+SLOTS = 16       # stamps per block: 0 start, 1-8 wave ends, 9-15 the merge phases
+
+
+def stamps_of(s: Setup, steps: int = 200) -> dict:
+    import numpy as np
+    import torch
+    lib = core.load()
+    if not hasattr(lib, "pa_debug_stamps"):
+        raise SystemExit("the loaded library has no stamps: build it with -D PA_STAMPS=1 and set PA_DECODE_LIB")
+    lib.pa_debug_stamps.argtypes = [ctypes.c_void_p, ctypes.c_ulong]
+    stream = torch.cuda.current_stream()
+    sh = stream.cuda_stream
+    for _ in range(50):
+        s.run(sh)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for _ in range(steps):
+        s.run(sh)
+    b.record(stream)
+    b.synchronize()
+    nb = (s.plan.num_ctas + 7) // 8
+    buf = np.zeros(nb * SLOTS, np.uint64)
+    if lib.pa_debug_stamps(buf.ctypes.data, buf.nbytes) != 0:
+        raise RuntimeError("pa_debug_stamps failed")
+    st = buf.reshape(nb, SLOTS).astype(np.int64)
+    t0 = st[:, 0].min()
+
+    def us(x):
+        return (x - t0) * TICK_US
+
+    def p50_max(x):
+        return [round(float(np.median(x)), 2), round(float(np.max(x)), 2)] if len(x) else None
+
+    wend = st[:, 1:9]
+    blk_end = wend.max(1)
+    r = {"batch": s.batch, "len": s.lens[0], "dtype": "fp8_e4m3" if s.fp8 else "fp16",
+         "block_merge": int(s.params.block_merge), "blocks": nb,
+         "period_us": round(a.elapsed_time(b) * 1e3 / steps, 2),
+         "wave_end": [round(float(np.percentile(us(wend), q)), 2) for q in (0, 50, 100)]}
+    last_end = us(blk_end).max()
+    if s.params.block_merge == 2:
+        arr = st[:, 9] > 0
+        last = st[:, 15] > st[:, 11]
+        r["merge_in_block"] = p50_max((st[arr, 9] - blk_end[arr]) * TICK_US)
+        r["store_wait"] = p50_max((st[arr, 10] - st[arr, 9]) * TICK_US)
+        r["arrive"] = p50_max((st[arr, 11] - st[arr, 10]) * TICK_US)
+        r["combine"] = [round(float(np.median((st[last, k + 1] - st[last, k]) * TICK_US)), 2)
+                        for k in (11, 12, 13, 14)] if last.any() else None
+        r["combining_blocks"] = int(last.sum())
+        if last.any():
+            last_end = max(last_end, us(st[last, 15]).max())
+    r["last_end"] = round(float(last_end), 2)
+    return r
+
+
+def main(argv: list[str] | None = None) -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--shape", nargs=3, action="append", metavar=("BATCH", "LEN", "DTYPE"))
+    ap.add_argument("--merge-kernel", action="store_true", help="force the merge kernel (block_merge 0)")
+    o = ap.parse_args(sys.argv[1:] if argv is None else argv)
+    shapes = o.shape or [("4", "1024", "fp16"), ("2", "16384", "fp16"), ("1", "131072", "fp16"),
+                         ("1", "131072", "fp8")]
+    import torch
+    torch.cuda.init()
+    core.load()
+    for b, length, dt in shapes:
+        s = Setup([int(length)] * int(b), fp8=dt == "fp8")
+        if o.merge_kernel and s.params.block_merge != 0:
+            s.params.block_merge, s.params.needs_merge = 0, 1
+        print(json.dumps(stamps_of(s)), flush=True)
+        s.close()
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

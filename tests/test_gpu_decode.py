@@ -272,6 +272,68 @@ def test_block_merge_two_split_segments_per_unit(fp8, group):
         assert float(np.max(np.abs(o - ref))) < TOL
     assert float(np.max(np.abs(outs[0] - outs[1]))) < 1e-3
 
+def _device_ints(ptr, n):
+    """n int32 from device memory (synchronous hipMemcpy)."""
+    import ctypes
+    hip = ctypes.CDLL("libamdhip64.so")
+    hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    out = np.zeros(n, np.int32)
+    assert hip.hipMemcpy(out.ctypes.data, ptr, 4 * n, 2) == 0   # hipMemcpyDeviceToHost
+    return out
+
+@pytest.mark.parametrize("lens,ctas,group", [
+    ([1024] * 4, 0, 4),                    # C1's shape on the default grid: 8 blocks per item
+    ([16384, 16384], 0, 4),                # 16 blocks per item, the most the split kernel merges
+    ([300, 4100, 17, 9000, 2500, 7000, 12000, 5000], 0, 4),   # ragged: items of 1 to 10 blocks
+    ([3000, 5000, 64], 150, 1),            # G = 1 (a block merges fewer elements than threads)
+    ([2048, 6000], 300, 2),
+    ([4096] * 3, 0, 8),                    # G = 8 (two elements per thread)
+    ([100] * 40 + [12000], 500, 4),        # many short whole items and one long split one
+], ids=["c1", "two_rows", "ragged", "g1", "g2", "g8", "short_and_long"])
+@pytest.mark.parametrize("fp8", DTYPES, ids=IDS)
+def test_chained_merge_matches_merge_kernel(fp8, lens, ctas, group):
+    """Plans whose split items span blocks are merged inside the split kernel
+    (block_merge 2: block partials, per-item arrival counters, the last block
+    combines). Against the merge kernel on the same plan and the oracle; two
+    runs are bitwise equal (the combine order does not depend on which block
+    finishes last), and the counters are back at zero after each decode."""
+    import torch
+    hkv = 8
+    hq = hkv * group
+    dt = pa_amd.FP8_E4M3 if fp8 else pa_amd.FP16
+    q, k, v, table, ks, vs = paged_inputs(len(lens), lens, hq, hkv, 16, fp8, seed=61 + group + len(lens))
+    plan = pa_amd.make_plan(dt, lens, hq, hkv, D, ctas)
+    assert plan.merge_mode == 2
+    dplan = pa_amd.DevicePlan()
+    dplan.upload(plan, group, D)
+    outs = []
+    for force_kernel in (False, False, True):
+        p = pa_amd.DecodeParams()
+        p.q, p.k_cache, p.v_cache, p.block_table = q.data_ptr(), k.data_ptr(), v.data_ptr(), table.data_ptr()
+        out = torch.full_like(q, float("nan"))
+        p.out = out.data_ptr()
+        p.block_table_stride = table.size(1)
+        p.batch, p.num_q_heads, p.num_kv_heads, p.head_dim, p.page_size = len(lens), hq, hkv, D, 16
+        p.sm_scale, p.k_scale, p.v_scale = pa_amd.sm_scale(D), ks, vs
+        dplan.bind(p)
+        assert p.block_merge == 2 and p.needs_merge == 0 and p.merge_counters
+        if force_kernel:
+            p.block_merge, p.needs_merge = 0, 1
+        pa_amd.paged_decode(dt, p)
+        torch.cuda.synchronize()
+        assert not _device_ints(p.merge_counters, len(lens) * hkv).any()
+        outs.append(out)
+    assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
+    kb = k.view(torch.uint8).cpu().numpy() if fp8 else k.view(torch.int16).cpu().numpy().view(np.uint16)
+    vb = v.view(torch.uint8).cpu().numpy() if fp8 else v.view(torch.int16).cpu().numpy().view(np.uint16)
+    ref = oracle.paged_decode(dt, q.view(torch.int16).cpu().numpy().view(np.uint16), kb, vb, table.cpu().numpy(),
+                              np.asarray(lens, np.int32), hq, hkv, D, 16, ks, vs, threads=16)
+    res = [o.float().cpu().numpy() for o in outs]
+    for o in res:
+        assert np.isfinite(o).all()
+        assert float(np.max(np.abs(o - ref))) < TOL
+    assert float(np.max(np.abs(res[0] - res[2]))) < 1e-3
+
 @pytest.mark.parametrize("lens", [[1024] * 4, [20000], [300, 4100, 17]], ids=["c1", "long", "ragged"])
 def test_graph_capture_replays_match_eager(lens):
     """A decode step (PagedKVCache::run: split + merge launches) captured into

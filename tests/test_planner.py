@@ -144,3 +144,93 @@ def test_plan_create_accepts_built_plans_and_rejects_broken_ones():
     bad = dict(good, item=built.item_seg_begin.copy())
     bad["item"][-1] += 1                                           # does not end at num_segments
     assert _create(bad) == 1
+
+
+def _created_mode(plan, num_kv_heads=0):
+    """merge mode of a caller-built plan (pa_plan_create), or None if refused."""
+    import ctypes
+    lib = pa_amd._lib.load()
+    h = ctypes.c_void_p()
+    seg = np.ascontiguousarray(plan["segments"], np.int32)
+    cta = np.ascontiguousarray(plan["cta"], np.int32)
+    itm = np.ascontiguousarray(plan["item"], np.int32)
+    if lib.pa_plan_create(plan["num_ctas"], plan["tile"], seg.ctypes.data, len(seg), cta.ctypes.data,
+                          itm.ctypes.data, len(itm) - 1, num_kv_heads, ctypes.byref(h)) != 0:
+        return None
+    out = ctypes.c_int(-1)
+    assert lib.pa_plan_merge_mode(h.value, ctypes.byref(out)) == 0
+    lib.pa_plan_destroy(h.value)
+    return out.value
+
+
+@pytest.mark.parametrize("lens,units,tile,mode", [
+    ([1024] * 4, 2048, 16, 2),        # C1 on the full grid: 8 blocks per (row, kv head)
+    ([8192] * 32, 2048, 16, 1),       # C2: 8 units per item, one block each
+    ([8192] * 64, 2048, 32, 1),       # C3 (FP8 step)
+    ([131072], 2048, 16, 0),          # C5: 32 blocks per item, past the split kernel's limit of 16
+    ([65536] * 2, 2048, 16, 2),       # 16 blocks per item
+    ([8192] * 32, 256, 16, 0),        # one unit per item: nothing split
+    ([700, 33, 2000], 100, 16, 2),
+])
+def test_merge_mode_of_make_plan_cuts(lens, units, tile, mode):
+    """Every make_plan cut keeps an item's segments in consecutive units, each
+    the first or last of its unit, so the split kernel merges every split
+    item itself: inside one block (1) or across blocks (2)."""
+    plan = pa_amd.make_plan_tiled(tile, lens, 8, units)
+    assert plan.merge_mode == mode
+    n = len(plan.item_seg_begin) - 1
+    if mode:
+        assert len(plan.segments) > n
+        unit_of = np.repeat(np.arange(plan.num_ctas), np.diff(plan.cta_seg_begin))
+        for i in range(n):
+            a, z = int(plan.item_seg_begin[i]), int(plan.item_seg_begin[i + 1])
+            assert list(unit_of[a:z]) == list(range(unit_of[a], unit_of[a] + z - a))
+
+
+def _expected_mode(plan):
+    """The merge mode restated from the schedule: nothing split -> 0; every
+    split item inside one block of 8 units -> 1; every split item over at most
+    16 blocks -> 2 (make_plan cuts always keep an item's segments in
+    consecutive units); else 0."""
+    n = len(plan.item_seg_begin) - 1
+    if len(plan.segments) <= n:
+        return 0
+    unit_of = np.repeat(np.arange(plan.num_ctas), np.diff(plan.cta_seg_begin))
+    nbs = [unit_of[z - 1] // 8 - unit_of[a] // 8 + 1
+           for a, z in zip(plan.item_seg_begin[:-1], plan.item_seg_begin[1:]) if z - a > 1]
+    return 1 if max(nbs) == 1 else 2 if max(nbs) <= 16 else 0
+
+
+def test_merge_mode_of_ragged_make_plan_cuts():
+    rng = np.random.default_rng(4)
+    lens = [int(x) for x in rng.integers(128, 16385, size=128)]   # C4
+    assert pa_amd.make_plan_tiled(16, lens, 8, 2048).merge_mode == 2
+    modes = set()
+    for seed in range(40):
+        rng = np.random.default_rng(100 + seed)
+        lens = [int(x) for x in rng.integers(1, 40000, size=int(rng.integers(1, 40)))]
+        plan = pa_amd.make_plan_tiled(16, lens, int(rng.choice([1, 2, 4, 8])), int(rng.integers(1, 3000)))
+        assert plan.merge_mode == _expected_mode(plan)
+        modes.add(plan.merge_mode)
+    assert modes == {0, 1, 2}
+
+
+def test_merge_mode_of_caller_plans():
+    """Caller-built plans the split kernel cannot merge fall back to the merge
+    kernel (0): an item whose segments skip a unit across blocks, and a split
+    segment in the middle of a unit."""
+    # hkv 1: item 0 = 64 tokens in units 0 and 9 (units 1..8 empty), item 1 whole.
+    skip = dict(num_ctas=10, tile=16,
+                segments=[[0, 0, 0, 32], [0, 0, 32, 64], [1, 0, 0, 32]],
+                cta=[0, 1, 1, 1, 1, 1, 1, 1, 1, 1, 3], item=[0, 2, 3])
+    assert _created_mode(skip, 1) == 0
+    skip_in_block = dict(skip, num_ctas=3, cta=[0, 1, 1, 3])    # the same inside one block
+    assert _created_mode(skip_in_block, 1) == 1
+    # item 1 split twice inside unit 1: its first part is neither first nor last there.
+    middle = dict(num_ctas=3, tile=16,
+                  segments=[[0, 0, 0, 32], [0, 0, 32, 48], [1, 0, 0, 16], [1, 0, 16, 32], [1, 0, 32, 48],
+                            [2, 0, 0, 16]],
+                  cta=[0, 1, 5, 6], item=[0, 2, 5, 6])
+    assert _created_mode(middle, 1) == 0
+    whole = dict(num_ctas=2, tile=16, segments=[[0, 0, 0, 32], [1, 0, 0, 16]], cta=[0, 1, 2], item=[0, 1, 2])
+    assert _created_mode(whole, 1) == 0                          # nothing to merge

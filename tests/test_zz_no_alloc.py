@@ -54,6 +54,10 @@ def test_decode_static_refuses_oversized_plans_without_a_device():
     p.num_segments, p.needs_merge = too_many, 1
     assert lib.pa_decode_static(0, ctypes.byref(p), too_many, None) == _lib.PA_ERR_LENGTH
     assert b"static scratch" in lib.pa_last_error()
+    p.needs_merge, p.block_merge = 0, 2                 # merged across blocks: partials in the array too
+    assert lib.pa_decode_static(0, ctypes.byref(p), too_many, None) == _lib.PA_ERR_LENGTH
+    assert b"static scratch" in lib.pa_last_error()
+    p.needs_merge, p.block_merge = 1, 0
     assert lib.pa_decode_static(0, None, 10, None) == _lib.PA_ERR_INVALID_ARGUMENT
     # An understated count: the kernels would write the bound plan's partials.
     p.num_segments = 2048
@@ -98,23 +102,28 @@ def test_decode_static_matches_decode_on_two_calls(fp8):
     lib = _lib.load()
     hq, hkv = 32, 8
     dt = pa_amd.FP8_E4M3 if fp8 else pa_amd.FP16
-    # Call 1: 4 x 1024 on the default grid (rows split across blocks: merge
-    # kernel). Call 2, smaller: a ragged batch on 100 units. Call 3: 8 x 2048
-    # on 512 units, merged inside the split kernel (no workspace).
-    cases = [([1024] * 4, 0, False), ([700, 33, 2000], 100, False), ([2048] * 8, 512, True)]
+    # Call 1: 4 x 1024 on the default grid (rows split across blocks, merged
+    # by the split kernel through block partials in the array). Call 2,
+    # smaller: a ragged batch on 100 units, forced through the merge kernel
+    # (every segment's partial in the array). Call 3: 8 x 2048 on 512 units,
+    # merged inside one block each (no workspace).
+    cases = [([1024] * 4, 0, 2, False), ([700, 33, 2000], 100, 2, True), ([2048] * 8, 512, 1, False)]
     prev_segments = None
-    for i, (lens, ctas, merged) in enumerate(cases):
+    for i, (lens, ctas, mode, force_kernel) in enumerate(cases):
         q, k, v, table, ks, vs = paged_inputs(len(lens), lens, hq, hkv, 16, fp8, seed=40 + i)
         plan = pa_amd.make_plan(dt, lens, hq, hkv, D, ctas)
         nseg = len(plan.segments)
-        if prev_segments is not None and not merged:
+        if prev_segments is not None and mode != 1:
             assert nseg < prev_segments                # the second call is the smaller input
         prev_segments = nseg
         dplan = pa_amd.DevicePlan()
         dplan.upload(plan, hq // hkv, D)
         p_ref, out_ref = _params(q, k, v, table, lens, hq, hkv, ks, vs, dplan)
-        assert (p_ref.block_merge == 1) == merged and (p_ref.needs_merge == 1) == (not merged)
+        assert p_ref.block_merge == mode and p_ref.needs_merge == 0
         p_st, out_st = _params(q, k, v, table, lens, hq, hkv, ks, vs, dplan)
+        if force_kernel:
+            for p in (p_ref, p_st):
+                p.block_merge, p.needs_merge = 0, 1
         p_st.partial_out = None                        # ignored by the static entry point
         p_st.partial_lse = None
         out_st.fill_(float("nan"))
@@ -138,10 +147,12 @@ def test_decode_static_matches_decode_on_two_calls(fp8):
 
 @pytest.mark.gpu
 @pytest.mark.usefixtures("gpu_device")
-def test_decode_static_graph_replays_match_eager():
+@pytest.mark.parametrize("force_kernel", [False, True], ids=["split_kernel_merge", "merge_kernel"])
+def test_decode_static_graph_replays_match_eager(force_kernel):
     """The callers the entry point is for: pa_decode_static captured into a HIP
-    graph, on a plan whose rows span blocks (the merge kernel reads the
-    library's array). Every replay, with q rewritten before it and an eager
+    graph, on a plan whose rows span blocks (block partials in the library's
+    array, merged by the split kernel; or, forced, every partial there for the
+    merge kernel). Every replay, with q rewritten before it and an eager
     pa_decode_static of other inputs after it (the same array, the same
     stream), equals an eager pa_decode of the same q with the plan's own
     workspace, bitwise."""
@@ -155,11 +166,14 @@ def test_decode_static_graph_replays_match_eager():
     dplan = pa_amd.DevicePlan()
     dplan.upload(plan, hq // hkv, D)
     p_ref, out_ref = _params(q, k, v, table, lens, hq, hkv, ks, vs, dplan)
-    assert p_ref.needs_merge == 1 and p_ref.block_merge == 0
+    assert p_ref.needs_merge == 0 and p_ref.block_merge == 2
     p_st, out_st = _params(q, k, v, table, lens, hq, hkv, ks, vs, dplan)
     g = torch.Generator(device="cuda").manual_seed(5)
     other_q = torch.randn(q.shape, device="cuda", dtype=q.dtype, generator=g)
     p_other, _ = _params(other_q, k, v, table, lens, hq, hkv, ks, vs, dplan)
+    if force_kernel:
+        for p in (p_ref, p_st, p_other):
+            p.block_merge, p.needs_merge = 0, 1
     st = torch.cuda.Stream()
     with torch.cuda.stream(st):
         h = st.cuda_stream
@@ -204,7 +218,7 @@ def params(out):
     return p
 out_ref, out_st = torch.empty_like(q), torch.zeros_like(q)
 p_ref, p_st = params(out_ref), params(out_st)
-assert p_ref.needs_merge == 1
+assert p_ref.block_merge == 2
 st = torch.cuda.Stream()
 with torch.cuda.stream(st):
     graph = torch.cuda.CUDAGraph()
