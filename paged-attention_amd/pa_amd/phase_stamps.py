@@ -14,6 +14,8 @@ One JSON line per shape:
 
   period_us          one step back to back (kernel plus the gap to the next)
   wave_end           p0 / p50 / p100 of the waves' ends of their split loop
+  block_mean_end     p0 / p50 / p100 over blocks of their waves' mean end
+  xcd_mean_end       that mean per XCD (blocks b, b + 8, ... run on XCD b % 8)
   merge_in_block     per block, from its last wave's end to its merged items
                      (the LDS merge, and for items that span blocks the
                      partial row stored)
@@ -75,10 +77,13 @@ def stamps_of(s: Setup, steps: int = 200) -> dict:
 
     wend = st[:, 1:9]
     blk_end = wend.max(1)
-    r = {"batch": s.batch, "len": s.lens[0], "dtype": "fp8_e4m3" if s.fp8 else "fp16",
+    cu_mean = us(wend).mean(1)   # one block per CU: its waves' mean end
+    r = {"batch": s.batch, "len": s.lens[0], "dtype": "fp8_e4m3" if s.fp8 else "fp16", "page": s.page,
          "block_merge": int(s.params.block_merge), "blocks": nb,
          "period_us": round(a.elapsed_time(b) * 1e3 / steps, 2),
-         "wave_end": [round(float(np.percentile(us(wend), q)), 2) for q in (0, 50, 100)]}
+         "wave_end": [round(float(np.percentile(us(wend), q)), 2) for q in (0, 50, 100)],
+         "block_mean_end": [round(float(np.percentile(cu_mean, q)), 2) for q in (0, 50, 100)],
+         "xcd_mean_end": [round(float(cu_mean[x::8].mean()), 2) for x in range(8)] if nb % 8 == 0 else None}
     last_end = us(blk_end).max()
     if s.params.block_merge == 2:
         arr = st[:, 9] > 0
@@ -99,6 +104,8 @@ def main(argv: list[str] | None = None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--shape", nargs=3, action="append", metavar=("BATCH", "LEN", "DTYPE"))
     ap.add_argument("--merge-kernel", action="store_true", help="force the merge kernel (block_merge 0)")
+    ap.add_argument("--page", type=int, default=16, help="tokens per page")
+    ap.add_argument("--contiguous-pages", action="store_true", help="no free-list shuffle (pages in memory order)")
     o = ap.parse_args(sys.argv[1:] if argv is None else argv)
     shapes = o.shape or [("4", "1024", "fp16"), ("2", "16384", "fp16"), ("1", "131072", "fp16"),
                          ("1", "131072", "fp8")]
@@ -106,7 +113,7 @@ def main(argv: list[str] | None = None) -> int:
     torch.cuda.init()
     core.load()
     for b, length, dt in shapes:
-        s = Setup([int(length)] * int(b), fp8=dt == "fp8")
+        s = Setup([int(length)] * int(b), page=o.page, fp8=dt == "fp8", shuffle=not o.contiguous_pages)
         if o.merge_kernel and s.params.block_merge != 0:
             s.params.block_merge, s.params.needs_merge = 0, 1
         print(json.dumps(stamps_of(s)), flush=True)
