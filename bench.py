@@ -355,6 +355,9 @@ def device_report(dev: int = 0) -> dict:
                 # the runtime reports a 2 GHz memory clock, so on MI355X the
                 # formula gives half of that.
                 "formula_peak_gbps": round(2.0 * clock_khz * 1e3 * bus_bits / 8 / 1e9, 1),
+                "formula_note": "2 x memory clock x bus width (bench_decode.cu:87-100); the runtime's memory "
+                                "clock understates HBM3E's 8 Gb/s per pin, so peak_gbps stays the published "
+                                f"{PEAK_GBPS:.0f} GB/s",
                 "source": "HIP runtime (hipGetDeviceProperties, hipDeviceGetAttribute)"}
     except (OSError, RuntimeError, AttributeError, ValueError) as e:
         return {"source": f"HIP device query failed ({type(e).__name__})"}
