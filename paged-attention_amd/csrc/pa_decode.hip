@@ -59,7 +59,7 @@
 //     after one barrier every thread of the block merges one head-dim element
 //     of each split row. A row inside the block (e.g. 32 rows x 8 kv heads x
 //     8192 tokens over 2048 units) is then complete; a row that spans blocks
-//     (up to 16) leaves one device-coherent partial per block, and the last
+//     (up to 8) leaves one device-coherent partial per block, and the last
 //     of its blocks to arrive (a per-row counter) combines them, in block
 //     order. No merge launch is needed. Otherwise (rows over more blocks, or
 //     caller plans that do not keep a row's segments in consecutive units)

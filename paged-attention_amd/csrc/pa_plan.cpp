@@ -105,7 +105,7 @@ void check_dtype(int dtype) {
     if (dtype != PA_KV_FP16 && dtype != PA_KV_FP8_E4M3)
         throw std::invalid_argument("unknown kv dtype " + std::to_string(dtype));
 }
-constexpr int kChainMaxBlocks = 16;   // blocks one item may span under block_merge 2
+constexpr int kChainMaxBlocks = 8;    // blocks one item may span under block_merge 2
 int plan_merge_mode(const pa_plan& plan) {
     const size_t nseg = plan.segments.size() / 4;
     if (nseg <= static_cast<size_t>(plan.items)) return 0;   // no split items
@@ -123,11 +123,13 @@ int plan_merge_mode(const pa_plan& plan) {
         const int nb = unit_of[static_cast<size_t>(z - 1)] / pa::kBlockUnits - u0 / pa::kBlockUnits + 1;
         if (nb > 1) in_block = false;
         // The split kernel's combine of a spanning item runs on one CU and
-        // reads one partial per block: past 16 blocks per item the merge
-        // kernel, which spreads every item over many CUs, is faster (one
-        // MI355X, fp16 and FP8: 16 blocks per item 1.0-1.3 us faster in the
-        // split kernel, 32 blocks 0.5-2.7 us slower). It addresses the
-        // partial rows with 32-bit offsets (segments x 8 heads x 128 floats).
+        // reads one partial per block: past 8 blocks per item the merge
+        // kernel, which spreads every item over many CUs, is as fast or
+        // faster (one MI355X: at 16 blocks per item 0.4-1.3 us faster in the
+        // split kernel back to back but 0.9-1.6 us slower after a cache
+        // flush, and slower either way on half-filled grids; at 32 blocks
+        // 0.5-2.7 us slower). It addresses the partial rows with 32-bit
+        // offsets (segments x 8 heads x 128 floats).
         if (nb > kChainMaxBlocks || z - a >= (1 << 19)) consecutive = false;
         for (int sg = a; sg < z; ++sg) {
             const int u = unit_of[static_cast<size_t>(sg)];

@@ -12,7 +12,8 @@ events: the period of one step), and the stamps of the last step are read
 back. Times are microseconds after the first block started (100 MHz clock).
 One JSON line per shape:
 
-  period_us          one step back to back (kernel plus the gap to the next)
+  period_us          one step back to back (kernel plus the gap to the next);
+                     with --cold, cold_step_us: the median step after a 1 GiB flush
   wave_end           p0 / p50 / p100 of the waves' ends of their split loop
   block_mean_end     p0 / p50 / p100 over blocks of their waves' mean end
   xcd_mean_end       that mean per XCD (blocks b, b + 8, ... run on XCD b % 8)
@@ -38,13 +39,13 @@ import json
 import sys
 
 from . import core
-from .bench_decode import Setup
+from .bench_decode import Flusher, Setup
 
 TICK_US = 0.01   # s_memrealtime runs at 100 MHz
 SLOTS = 16       # stamps per block: 0 start, 1-8 wave ends, 9-15 the merge phases
 
 
-def stamps_of(s: Setup, steps: int = 200) -> dict:
+def stamps_of(s: Setup, steps: int = 200, flusher: Flusher | None = None) -> dict:
     import numpy as np
     import torch
     lib = core.load()
@@ -57,11 +58,25 @@ def stamps_of(s: Setup, steps: int = 200) -> dict:
         s.run(sh)
     torch.cuda.synchronize()
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    a.record(stream)
-    for _ in range(steps):
-        s.run(sh)
-    b.record(stream)
-    b.synchronize()
+    if flusher is None:
+        a.record(stream)
+        for _ in range(steps):
+            s.run(sh)
+        b.record(stream)
+        b.synchronize()
+        period_ms = a.elapsed_time(b) / steps
+    else:
+        # The reference's cold method: a 1 GiB read before every step, events
+        # around the step alone; the median step.
+        ms = []
+        for _ in range(steps // 4):
+            flusher.flush(stream)
+            a.record(stream)
+            s.run(sh)
+            b.record(stream)
+            b.synchronize()
+            ms.append(a.elapsed_time(b))
+        period_ms = sorted(ms)[len(ms) // 2]
     nb = (s.plan.num_ctas + 7) // 8
     buf = np.zeros(nb * SLOTS, np.uint64)
     if lib.pa_debug_stamps(buf.ctypes.data, buf.nbytes) != 0:
@@ -80,7 +95,7 @@ def stamps_of(s: Setup, steps: int = 200) -> dict:
     cu_mean = us(wend).mean(1)   # one block per CU: its waves' mean end
     r = {"batch": s.batch, "len": s.lens[0], "dtype": "fp8_e4m3" if s.fp8 else "fp16", "page": s.page,
          "block_merge": int(s.params.block_merge), "blocks": nb,
-         "period_us": round(a.elapsed_time(b) * 1e3 / steps, 2),
+         "period_us" if flusher is None else "cold_step_us": round(period_ms * 1e3, 2),
          "wave_end": [round(float(np.percentile(us(wend), q)), 2) for q in (0, 50, 100)],
          "block_mean_end": [round(float(np.percentile(cu_mean, q)), 2) for q in (0, 50, 100)],
          "xcd_mean_end": [round(float(cu_mean[x::8].mean()), 2) for x in range(8)] if nb % 8 == 0 else None}
@@ -106,17 +121,19 @@ def main(argv: list[str] | None = None) -> int:
     ap.add_argument("--merge-kernel", action="store_true", help="force the merge kernel (block_merge 0)")
     ap.add_argument("--page", type=int, default=16, help="tokens per page")
     ap.add_argument("--contiguous-pages", action="store_true", help="no free-list shuffle (pages in memory order)")
+    ap.add_argument("--cold", action="store_true", help="a 1 GiB flush before every step (the stamps are the last step's)")
     o = ap.parse_args(sys.argv[1:] if argv is None else argv)
     shapes = o.shape or [("4", "1024", "fp16"), ("2", "16384", "fp16"), ("1", "131072", "fp16"),
                          ("1", "131072", "fp8")]
     import torch
     torch.cuda.init()
     core.load()
+    flusher = Flusher() if o.cold else None
     for b, length, dt in shapes:
         s = Setup([int(length)] * int(b), page=o.page, fp8=dt == "fp8", shuffle=not o.contiguous_pages)
         if o.merge_kernel and s.params.block_merge != 0:
             s.params.block_merge, s.params.needs_merge = 0, 1
-        print(json.dumps(stamps_of(s)), flush=True)
+        print(json.dumps(stamps_of(s, flusher=flusher)), flush=True)
         s.close()
     return 0
 

@@ -283,11 +283,11 @@ def _device_ints(ptr, n):
 
 @pytest.mark.parametrize("lens,ctas,group", [
     ([1024] * 4, 0, 4),                    # C1's shape on the default grid: 8 blocks per item
-    ([16384, 16384], 0, 4),                # 16 blocks per item, the most the split kernel merges
-    ([300, 4100, 17, 9000, 2500, 7000, 12000, 5000], 0, 4),   # ragged: items of 1 to 10 blocks
+    ([16384] * 4, 0, 4),                   # 8 blocks per item, the most the split kernel merges
+    ([300, 4100, 17, 9000, 2500, 7000, 12000, 5000, 6000, 9000], 0, 4),   # ragged: items of 1 to 8 blocks
     ([3000, 5000, 64], 150, 1),            # G = 1 (a block merges fewer elements than threads)
     ([2048, 6000], 300, 2),
-    ([4096] * 3, 0, 8),                    # G = 8 (two elements per thread)
+    ([4096] * 6, 0, 8),                    # G = 8 (two elements per thread)
     ([100] * 40 + [12000], 500, 4),        # many short whole items and one long split one
 ], ids=["c1", "two_rows", "ragged", "g1", "g2", "g8", "short_and_long"])
 @pytest.mark.parametrize("fp8", DTYPES, ids=IDS)

@@ -167,8 +167,9 @@ def _created_mode(plan, num_kv_heads=0):
     ([1024] * 4, 2048, 16, 2),        # C1 on the full grid: 8 blocks per (row, kv head)
     ([8192] * 32, 2048, 16, 1),       # C2: 8 units per item, one block each
     ([8192] * 64, 2048, 32, 1),       # C3 (FP8 step)
-    ([131072], 2048, 16, 0),          # C5: 32 blocks per item, past the split kernel's limit of 16
-    ([65536] * 2, 2048, 16, 2),       # 16 blocks per item
+    ([131072], 2048, 16, 0),          # C5: 32 blocks per item, past the split kernel's limit of 8
+    ([65536] * 2, 2048, 16, 0),       # 16 blocks per item
+    ([32768] * 4, 2048, 16, 2),       # 8 blocks per item
     ([8192] * 32, 256, 16, 0),        # one unit per item: nothing split
     ([700, 33, 2000], 100, 16, 2),
 ])
@@ -190,7 +191,7 @@ def test_merge_mode_of_make_plan_cuts(lens, units, tile, mode):
 def _expected_mode(plan):
     """The merge mode restated from the schedule: nothing split -> 0; every
     split item inside one block of 8 units -> 1; every split item over at most
-    16 blocks -> 2 (make_plan cuts always keep an item's segments in
+    8 blocks -> 2 (make_plan cuts always keep an item's segments in
     consecutive units); else 0."""
     n = len(plan.item_seg_begin) - 1
     if len(plan.segments) <= n:
@@ -198,7 +199,7 @@ def _expected_mode(plan):
     unit_of = np.repeat(np.arange(plan.num_ctas), np.diff(plan.cta_seg_begin))
     nbs = [unit_of[z - 1] // 8 - unit_of[a] // 8 + 1
            for a, z in zip(plan.item_seg_begin[:-1], plan.item_seg_begin[1:]) if z - a > 1]
-    return 1 if max(nbs) == 1 else 2 if max(nbs) <= 16 else 0
+    return 1 if max(nbs) == 1 else 2 if max(nbs) <= 8 else 0
 
 
 def test_merge_mode_of_ragged_make_plan_cuts():
