@@ -172,19 +172,32 @@ _lib: ctypes.CDLL | None = None
 
 
 def _init_torch_device_state() -> None:
-    """Lets torch set up its HIP state before this library loads.
+    """Loads torch's HIP runtime before this library's.
 
-    torch and libpa_decode.so share one HIP runtime in a Python process. On
-    the MI355X boxes, when the library was loaded (registering its code
-    objects) before torch's first device query, later HIP calls from one of
-    the two saw no device (hipErrorNoDevice); with torch first, both work. So
-    the library loads only after torch.cuda.is_available() has run (a no-op
-    without a GPU, and when torch is absent)."""
+    torch ships its own libamdhip64 (soname libamdhip64.so.7), and its
+    libraries ask for it as `libamdhip64.so`; this library asks for
+    `libamdhip64.so.7`. Loaded after torch, the library's request matches
+    torch's copy by soname and the process has one HIP runtime. Loaded first,
+    it brings in the system's copy (/opt/rocm), and torch's request, which no
+    loaded soname matches, then maps torch's own copy beside it: two HIP
+    runtimes in one process, of which the second finds no device
+    (hipErrorNoDevice, torch.cuda.is_available() False on the GPU boxes).
+    So torch goes first (a no-op when torch is absent)."""
     try:
         import torch
     except ImportError:
         return
     torch.cuda.is_available()
+
+
+def hip_runtimes() -> list[str]:
+    """Distinct HIP runtime libraries mapped into this process (Linux)."""
+    try:
+        maps = pathlib.Path("/proc/self/maps").read_text()
+    except OSError:
+        return []
+    paths = {line.split()[-1] for line in maps.splitlines() if "libamdhip64" in line}
+    return sorted({os.path.realpath(p) for p in paths})
 
 
 def load() -> ctypes.CDLL:
@@ -198,6 +211,11 @@ def load() -> ctypes.CDLL:
             "(or __graft_entry__.build()); there is no fallback path")
     _init_torch_device_state()
     lib = ctypes.CDLL(str(LIB_PATH))
+    runtimes = hip_runtimes()
+    if len(runtimes) > 1:
+        raise RuntimeError(
+            "two HIP runtimes are loaded in this process (" + ", ".join(runtimes) + "): libpa_decode.so was "
+            "loaded before torch; import torch (and query a device) before loading it")
     for name, (res, args) in SIGNATURES.items():
         fn = getattr(lib, name)
         fn.restype = res

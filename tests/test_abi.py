@@ -125,3 +125,47 @@ def test_compiled_torch_binding_loads_without_a_device():
     assert dec.num_ctas == 0 and dec.num_segments == 0
     with pytest.raises(RuntimeError, match="CPU int32"):
         dec.plan(torch.tensor([10], dtype=torch.int64))
+
+
+_BAD_ORDER = r"""
+import ctypes, sys
+sys.path[:0] = [sys.argv[1]]
+ctypes.CDLL(sys.argv[2])                  # the library first: the system's HIP runtime
+import torch                              # then torch: its own copy beside it
+from pa_amd import _lib
+assert len(_lib.hip_runtimes()) == 2, _lib.hip_runtimes()
+try:
+    _lib.load()
+except RuntimeError as e:
+    assert "two HIP runtimes" in str(e), e
+    print("refused")
+"""
+
+_GOOD_ORDER = r"""
+import sys
+sys.path[:0] = [sys.argv[1]]
+import torch
+from pa_amd import _lib
+_lib.load()
+assert len(_lib.hip_runtimes()) == 1, _lib.hip_runtimes()
+print("one runtime")
+"""
+
+
+def test_loader_refuses_a_second_hip_runtime():
+    """torch links its own copy of the HIP runtime and asks for it as
+    libamdhip64.so; the library asks for libamdhip64.so.7. Loaded after
+    torch, the library shares torch's copy; loaded before it, the process
+    ends up with two runtimes (the second sees no GPU), and pa_amd's loader
+    says so instead of failing later with hipErrorNoDevice. No GPU needed."""
+    import pathlib
+    import subprocess
+    import sys
+    pkg = pathlib.Path(pa_amd.__file__).resolve().parent.parent
+    lib = str(pkg / "lib" / "libpa_decode.so")
+    bad = subprocess.run([sys.executable, "-c", _BAD_ORDER, str(pkg), lib], capture_output=True, text=True,
+                         timeout=120)
+    assert bad.returncode == 0 and "refused" in bad.stdout, bad.stdout + bad.stderr[-2000:]
+    good = subprocess.run([sys.executable, "-c", _GOOD_ORDER, str(pkg)], capture_output=True, text=True,
+                          timeout=120)
+    assert good.returncode == 0 and "one runtime" in good.stdout, good.stdout + good.stderr[-2000:]
