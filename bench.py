@@ -375,6 +375,17 @@ EXTRA = [("c1", "c1", 16, True), ("c3", "c3", 16, True), ("c2_p16", "c2", 16, Tr
          ("c5fp8", "c5fp8", 16, True)]
 
 
+MERGE_NAMES = {0: "merge kernel", 1: "in the split kernel, inside one block",
+               2: "in the split kernel, across blocks"}
+
+
+def merge_of(s) -> str:
+    """How the plan's split rows are merged (pa_decode_params.block_merge)."""
+    if s.params.needs_merge == 0 and s.params.block_merge == 0:
+        return "none (no split rows)"
+    return MERGE_NAMES.get(int(s.params.block_merge), "?")
+
+
 def workload_figures(s, desc: str, steps: int, warmup: int, cold_iters: int, flusher) -> dict:
     """One workload's step (K back-to-back steps), split-kernel and cold figures."""
     wall, split_ms, region_ms = time_steps(s, steps, warmup)
@@ -382,7 +393,7 @@ def workload_figures(s, desc: str, steps: int, warmup: int, cold_iters: int, flu
     step_us = wall * 1e6 / steps
     split_us = (region_ms / steps if s.params.needs_merge == 0 else statistics.mean(split_ms)) * 1e3
     out = {"workload": desc, "page_size": s.page, "units": s.plan.num_ctas, "segments": int(len(s.plan.segments)),
-           "algorithmic_bytes": nbytes,
+           "merge": merge_of(s), "algorithmic_bytes": nbytes,
            "us_per_step": round(step_us, 2), "pct_of_peak": round(100 * nbytes / (step_us * 1e-6) / 1e9 / PEAK_GBPS, 2),
            "split_us": round(split_us, 2),
            "split_pct_of_peak": round(100 * nbytes / (split_us * 1e-6) / 1e9 / PEAK_GBPS, 2)}
@@ -509,6 +520,7 @@ def main() -> None:
             "kv_dtype": "fp8_e4m3" if fp8 else "fp16",
             "units": s.plan.num_ctas,
             "segments": int(len(s.plan.segments)),
+            "merge": merge_of(s),
             "algorithmic_bytes": nbytes,
         },
         "roofline": {

@@ -109,6 +109,7 @@ def test_bench_line_contract():
     assert d["n_gpus"] == 1 and d["steps"] == 3 and d["warmup"] == 1
     assert d["unit"] == "GB/s" and d["higher_is_better"] is True and d["dtype"] == "fp16"
     assert d["config"]["workload"].startswith("C2")
+    assert d["config"]["merge"] == "in the split kernel, inside one block"   # one launch per step
     # value is the algorithmic bytes of one step over the measured step time
     step_s = d["ms_per_step"] * 1e-3
     assert abs(d["config"]["algorithmic_bytes"] / step_s / 1e9 - d["value"]) / d["value"] < 0.01
