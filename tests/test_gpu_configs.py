@@ -220,6 +220,52 @@ def test_full_size_config2_page_size_sweep_bitwise(fp8):
         assert torch.equal(o.view(torch.int16), base), f"page size {P} differs from 16"
 
 
+@pytest.mark.parametrize("fp8", DTYPES, ids=IDS)
+def test_config1_page_size_sweep_bitwise(fp8):
+    """Config 1 (4 x 1024), whose rows span 8 blocks each and are merged across
+    blocks inside the split kernel: the same q/K/V in pages of 1, 4, 8, 16,
+    64 and 1024 tokens, each under its own page permutation, decode to
+    bitwise the same output (the block partials and their combine order do
+    not depend on where or how the pages sit), within tolerance of the oracle."""
+    import torch
+    B, L, hq, hkv = 4, 1024, 32, 8
+    g = torch.Generator(device="cuda").manual_seed(73)
+    if fp8:
+        def codes():
+            c = torch.randint(0, 0x7f, (B, hkv, L, D), device="cuda", generator=g, dtype=torch.int32).to(torch.uint8)
+            return c | (torch.randint(0, 2, c.shape, device="cuda", generator=g, dtype=torch.int32).to(torch.uint8) << 7)
+        klog, vlog = codes(), codes()
+        ks = vs = 4.0 / 448.0
+    else:
+        klog = torch.randn((B, hkv, L, D), device="cuda", dtype=torch.float16, generator=g)
+        vlog = torch.randn((B, hkv, L, D), device="cuda", dtype=torch.float16, generator=g)
+        ks = vs = 1.0
+    q = torch.randn((B, hq, D), device="cuda", dtype=torch.float16, generator=g)
+    lens = torch.full((B,), L, dtype=torch.int32)
+    dt = pa_amd.FP8_E4M3 if fp8 else pa_amd.FP16
+    assert pa_amd.make_plan(dt, [L] * B, hq, hkv, D, 0).merge_mode == 2
+    outs = {}
+    for P in (1, 4, 8, 16, 64, 1024):
+        perm = torch.randperm(B * (L // P), device="cuda", generator=torch.Generator(device="cuda").manual_seed(P))
+        perm = perm.to(torch.int32)
+        kp, table = _paged_layout(klog, P, perm)
+        vp, _ = _paged_layout(vlog, P, perm)
+        dec = pa_amd.Decoder(hq, hkv, D, P, fp8)
+        dec.plan(lens, 0)
+        outs[P] = dec.run(q, kp, vp, table, lens.cuda(), ks, vs)
+        torch.cuda.synchronize()
+        if P == 16:
+            kb = kp.cpu().numpy() if fp8 else kp.view(torch.int16).cpu().numpy().view(np.uint16)
+            vb = vp.cpu().numpy() if fp8 else vp.view(torch.int16).cpu().numpy().view(np.uint16)
+            ref = oracle.paged_decode(dt, q.view(torch.int16).cpu().numpy().view(np.uint16), kb, vb,
+                                      table.cpu().numpy(), lens.numpy(), hq, hkv, D, P, ks, vs, threads=16)
+            err = float(np.max(np.abs(outs[P].float().cpu().numpy() - ref)))
+            assert err < TOL, err
+    base = outs[16].view(torch.int16)
+    for P, o in outs.items():
+        assert torch.equal(o.view(torch.int16), base), f"page size {P} differs from 16"
+
+
 def test_full_size_config3_stored_fp8_bytes():
     """Config 3 at full size (64 x 8192): every FP8 byte the append kernel
     stored, at the run's own per-tensor scales (amax / 448 over the seeded

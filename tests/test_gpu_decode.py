@@ -292,6 +292,19 @@ def _device_ints(ptr, n):
 ], ids=["c1", "two_rows", "ragged", "g1", "g2", "g8", "short_and_long"])
 @pytest.mark.parametrize("fp8", DTYPES, ids=IDS)
 def test_chained_merge_matches_merge_kernel(fp8, lens, ctas, group):
+    _chained_case(fp8, lens, ctas, group, 16)
+
+
+@pytest.mark.parametrize("page", [1, 4, 8, 64])
+@pytest.mark.parametrize("fp8", DTYPES, ids=IDS)
+def test_chained_merge_every_page_path(fp8, page):
+    """The merge across blocks on every page path (per-lane lookups at 1
+    token per page, staged 1 KiB parts at 4 and 8, page runs at 64): 4 rows
+    of 1024 tokens over 8 blocks each."""
+    _chained_case(fp8, [1024] * 4, 0, 4, page)
+
+
+def _chained_case(fp8, lens, ctas, group, page):
     """Plans whose split items span blocks are merged inside the split kernel
     (block_merge 2: block partials, per-item arrival counters, the last block
     combines). Against the merge kernel on the same plan and the oracle; two
@@ -301,7 +314,7 @@ def test_chained_merge_matches_merge_kernel(fp8, lens, ctas, group):
     hkv = 8
     hq = hkv * group
     dt = pa_amd.FP8_E4M3 if fp8 else pa_amd.FP16
-    q, k, v, table, ks, vs = paged_inputs(len(lens), lens, hq, hkv, 16, fp8, seed=61 + group + len(lens))
+    q, k, v, table, ks, vs = paged_inputs(len(lens), lens, hq, hkv, page, fp8, seed=61 + group + len(lens) + page)
     plan = pa_amd.make_plan(dt, lens, hq, hkv, D, ctas)
     assert plan.merge_mode == 2
     dplan = pa_amd.DevicePlan()
@@ -313,7 +326,7 @@ def test_chained_merge_matches_merge_kernel(fp8, lens, ctas, group):
         out = torch.full_like(q, float("nan"))
         p.out = out.data_ptr()
         p.block_table_stride = table.size(1)
-        p.batch, p.num_q_heads, p.num_kv_heads, p.head_dim, p.page_size = len(lens), hq, hkv, D, 16
+        p.batch, p.num_q_heads, p.num_kv_heads, p.head_dim, p.page_size = len(lens), hq, hkv, D, page
         p.sm_scale, p.k_scale, p.v_scale = pa_amd.sm_scale(D), ks, vs
         dplan.bind(p)
         assert p.block_merge == 2 and p.needs_merge == 0 and p.merge_counters
@@ -327,7 +340,7 @@ def test_chained_merge_matches_merge_kernel(fp8, lens, ctas, group):
     kb = k.view(torch.uint8).cpu().numpy() if fp8 else k.view(torch.int16).cpu().numpy().view(np.uint16)
     vb = v.view(torch.uint8).cpu().numpy() if fp8 else v.view(torch.int16).cpu().numpy().view(np.uint16)
     ref = oracle.paged_decode(dt, q.view(torch.int16).cpu().numpy().view(np.uint16), kb, vb, table.cpu().numpy(),
-                              np.asarray(lens, np.int32), hq, hkv, D, 16, ks, vs, threads=16)
+                              np.asarray(lens, np.int32), hq, hkv, D, page, ks, vs, threads=16)
     res = [o.float().cpu().numpy() for o in outs]
     for o in res:
         assert np.isfinite(o).all()
