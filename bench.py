@@ -4,8 +4,9 @@
                     [--page-size P] [--ctas N] [--no-cpu] [--no-cold] [--no-copy]
 
 One step is one decode of one Llama-3-8B attention layer (Hq=32, Hkv=8,
-head_dim=128) over a paged KV cache: the split-KV decode kernel plus the LSE
-merge kernel, with the plan built once outside the timed region (the
+head_dim=128) over a paged KV cache: the split-KV decode kernel (which merges
+split rows itself when they span at most 8 blocks) plus the LSE merge kernel
+where a row spans more, with the plan built once outside the timed region (the
 reference's bench/bench_decode.cu:198-209). Inputs are synthetic and already
 resident in HBM: q/K/V ~ N(0,1) rounded to fp16, appended through the product's
 own append(-quantize) kernel into pages scattered by a seeded shuffle of the
