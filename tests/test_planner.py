@@ -186,6 +186,13 @@ def test_merge_mode_of_make_plan_cuts(lens, units, tile, mode):
         for i in range(n):
             a, z = int(plan.item_seg_begin[i]), int(plan.item_seg_begin[i + 1])
             assert list(unit_of[a:z]) == list(range(unit_of[a], unit_of[a] + z - a))
+            # The split kernel's addressing of a row's block partials: block j
+            # of the row keeps its partial at the row's first segment in j,
+            # a + max(0, 8 j - u0), for j from u0 // 8 to (u0 + n - 1) // 8.
+            u0 = int(unit_of[a])
+            for j in range(u0 // 8, (u0 + z - a - 1) // 8 + 1):
+                first = min(sg for sg in range(a, z) if unit_of[sg] // 8 == j)
+                assert first == a + max(0, 8 * j - u0)
 
 
 def _expected_mode(plan):
