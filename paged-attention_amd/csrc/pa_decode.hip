@@ -146,14 +146,14 @@
 #define PA_STAMPS 0
 #endif
 #if PA_STAMPS
-__device__ unsigned long long pa_stamps[4096 * 16];
+__device__ unsigned long long pa_stamps[4096 * 24];
 extern "C" int pa_debug_stamps(void* host, unsigned long bytes) {
     return static_cast<int>(hipMemcpyFromSymbol(host, HIP_SYMBOL(pa_stamps), bytes, 0, hipMemcpyDeviceToHost));
 }
 #endif
 __device__ __forceinline__ void stamp(int k) {
 #if PA_STAMPS
-    if ((threadIdx.x & 63) == 0 && blockIdx.x < 4096) pa_stamps[blockIdx.x * 16 + k] = __builtin_amdgcn_s_memrealtime();
+    if ((threadIdx.x & 63) == 0 && blockIdx.x < 4096) pa_stamps[blockIdx.x * 24 + k] = __builtin_amdgcn_s_memrealtime();
 #else
     (void)k;
 #endif
@@ -337,6 +337,7 @@ __device__ __forceinline__ void block_merge(const pa_decode_params& p, const int
     const int  lane  = tid & 63;
     const bool slot  = lane < NS;   // lane j holds slot j
     const bool chain = p.block_merge == 2;
+    if (tid == 0) stamp(16);
     float lv[NE], pv[NE][NS];
 #pragma unroll
     for (int e = 0; e < NE; ++e) {
@@ -349,6 +350,10 @@ __device__ __forceinline__ void block_merge(const pa_decode_params& p, const int
     }
     const int      mine   = slot_item[(lane & (NS - 1)) >> 1][lane & 1];
     const int      myseg  = slot_seg[(lane & (NS - 1)) >> 1][lane & 1];
+#if PA_STAMPS
+    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+    if (tid == 0) stamp(17);
+#endif
     const uint64_t filled = __builtin_amdgcn_ballot_w64(slot && mine >= 0);
     // Items of this block that span blocks (at most two), block-uniform.
     int ns = 0, sx0 = 0, su0 = 0, sn0 = 0, sx1 = 0, su1 = 0, sn1 = 0;
@@ -359,6 +364,9 @@ __device__ __forceinline__ void block_merge(const pa_decode_params& p, const int
         run = __builtin_amdgcn_ballot_w64(slot && mine == x);
         const int  n     = isb[x + 1] - isb[x];
         const bool spans = chain && __builtin_popcountll(run) != n;
+#if PA_STAMPS
+        if (tid == 0 && rem == filled) stamp(18 + spans);
+#endif
         const int  bseg  = __builtin_amdgcn_readlane(myseg, j0);   // the item's first segment here
         if (spans) {
             const int u0 = lblock * kWaves + (j0 >> 1) - (bseg - isb[x]);   // unit of its first segment

@@ -3,7 +3,7 @@ s_memrealtime stamps of its phases, from a diagnostic build of the library.
 
     python3 build.py -D PA_STAMPS=1 --lib lib/variants/libpa_decode_stamps.so
     PA_DECODE_LIB=lib/variants/libpa_decode_stamps.so \\
-        python3 -m pa_amd.phase_stamps [--shape B L fp16|fp8]... [--merge-kernel]
+        python3 -m pa_amd.phase_stamps [--shape B L fp16|fp8]... [--heads HQ HKV] [--merge-kernel]
 
 For each shape (default: 4 x 1024, 2 x 16384 and 1 x 131072, fp16 and FP8 for
 the last) a populated cache (bench_decode.Setup: 16-token shuffled pages, the
@@ -19,7 +19,10 @@ One JSON line per shape:
   xcd_mean_end       that mean per XCD (blocks b, b + 8, ... run on XCD b % 8)
   merge_in_block     per block, from its last wave's end to its merged items
                      (the LDS merge, and for items that span blocks the
-                     partial row stored)
+                     partial row stored), then its parts: barrier (to the
+                     merge's start), lds (the slots' partials read),
+                     count (the first item's segment count loaded), average
+                     (the weighted average computed, its stores issued)
   store_wait         those partial rows complete at the coherence point
   arrive             the arrival counter's round trip
   combine            the last block's combine of an item's block partials:
@@ -42,7 +45,7 @@ from . import core
 from .bench_decode import Flusher, Setup
 
 TICK_US = 0.01   # s_memrealtime runs at 100 MHz
-SLOTS = 16       # stamps per block: 0 start, 1-8 wave ends, 9-15 the merge phases
+SLOTS = 24       # stamps per block: 0 start, 1-8 wave ends, 9-15 and 16-19 the merge phases
 
 
 def stamps_of(s: Setup, steps: int = 200, flusher: Flusher | None = None) -> dict:
@@ -93,15 +96,24 @@ def stamps_of(s: Setup, steps: int = 200, flusher: Flusher | None = None) -> dic
     wend = st[:, 1:9]
     blk_end = wend.max(1)
     cu_mean = us(wend).mean(1)   # one block per CU: its waves' mean end
-    r = {"batch": s.batch, "len": s.lens[0], "dtype": "fp8_e4m3" if s.fp8 else "fp16", "page": s.page,
+    r = {"batch": s.batch, "len": s.lens[0], "hq": s.hq, "hkv": s.hkv,
+         "dtype": "fp8_e4m3" if s.fp8 else "fp16", "page": s.page,
          "block_merge": int(s.params.block_merge), "blocks": nb,
          "period_us" if flusher is None else "cold_step_us": round(period_ms * 1e3, 2),
          "wave_end": [round(float(np.percentile(us(wend), q)), 2) for q in (0, 50, 100)],
          "block_mean_end": [round(float(np.percentile(cu_mean, q)), 2) for q in (0, 50, 100)],
          "xcd_mean_end": [round(float(cu_mean[x::8].mean()), 2) for x in range(8)] if nb % 8 == 0 else None}
     last_end = us(blk_end).max()
+    if s.params.block_merge != 0:
+        ent = st[:, 16] > 0
+        cnt = np.maximum(st[:, 18], st[:, 19])
+        r["merge_barrier"] = p50_max((st[ent, 16] - blk_end[ent]) * TICK_US)
+        r["merge_lds"] = p50_max((st[ent, 17] - st[ent, 16]) * TICK_US)
+        r["merge_count"] = p50_max((cnt[ent] - st[ent, 17]) * TICK_US)
     if s.params.block_merge == 2:
         arr = st[:, 9] > 0
+        cnt = np.maximum(st[:, 18], st[:, 19])
+        r["merge_average"] = p50_max((st[arr, 9] - cnt[arr]) * TICK_US)
         last = st[:, 15] > st[:, 11]
         r["merge_in_block"] = p50_max((st[arr, 9] - blk_end[arr]) * TICK_US)
         r["store_wait"] = p50_max((st[arr, 10] - st[arr, 9]) * TICK_US)
@@ -118,6 +130,8 @@ def stamps_of(s: Setup, steps: int = 200, flusher: Flusher | None = None) -> dic
 def main(argv: list[str] | None = None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--shape", nargs=3, action="append", metavar=("BATCH", "LEN", "DTYPE"))
+    ap.add_argument("--heads", nargs=2, type=int, default=(32, 8), metavar=("HQ", "HKV"),
+                    help="query and kv heads (default 32 8; e.g. 4 1 for one GPU's share of 8-way head sharding)")
     ap.add_argument("--merge-kernel", action="store_true", help="force the merge kernel (block_merge 0)")
     ap.add_argument("--page", type=int, default=16, help="tokens per page")
     ap.add_argument("--contiguous-pages", action="store_true", help="no free-list shuffle (pages in memory order)")
@@ -130,7 +144,8 @@ def main(argv: list[str] | None = None) -> int:
     core.load()
     flusher = Flusher() if o.cold else None
     for b, length, dt in shapes:
-        s = Setup([int(length)] * int(b), page=o.page, fp8=dt == "fp8", shuffle=not o.contiguous_pages)
+        s = Setup([int(length)] * int(b), hq=o.heads[0], hkv=o.heads[1], page=o.page, fp8=dt == "fp8",
+                  shuffle=not o.contiguous_pages)
         if o.merge_kernel and s.params.block_merge != 0:
             s.params.block_merge, s.params.needs_merge = 0, 1
         print(json.dumps(stamps_of(s, flusher=flusher)), flush=True)
