@@ -42,6 +42,12 @@ COMMON = [
 
 SOURCES = ["pa_decode.hip", "pa_cache.hip", "pa_scratch.hip", "pa_plan.cpp", "pa_pool.cpp", "pa_kvcache.cpp"]
 
+# Device code only: the first kernel arguments (up to the first struct passed by
+# value) arrive preloaded in SGPRs when the wave starts, so a kernel's first
+# loads do not wait for a read of the kernel-argument segment. The code object
+# keeps an entry sequence that loads them for firmware without preloading.
+KERNARG_PRELOAD = ["-mllvm", "-amdgpu-kernarg-preload-count=8"]
+
 
 def _run(cmd: list[str]) -> None:
     proc = subprocess.run(cmd, capture_output=True, text=True)
@@ -63,7 +69,7 @@ def build(verbose: bool = False, defines: list[str] | None = None, lib: pathlib.
     objs = []
     for src in SOURCES:
         obj = obj_dir / (src + ".o")
-        lang = ["-x", "hip"] if src.endswith(".hip") else []
+        lang = ["-x", "hip", *KERNARG_PRELOAD] if src.endswith(".hip") else []
         jobs.append([HIPCC, *COMMON, *extra, *lang, "-c", str(CSRC / src), "-o", str(obj)])
         objs.append(obj)
     if verbose:
