@@ -1211,8 +1211,14 @@ void decode_split_kernel_fp8(const int32_t* __restrict__ cta, const int32_t* __r
 // a time. A single pass over the segments with a running base-2 maximum per
 // lane (no separate pass for the maximum: one dependent round trip fewer);
 // lanes of the same dims combine by shuffles, waves in LDS.
+//
+// The arrays it reads first come ahead of the params struct, preloaded in SGPRs
+// (as for the split kernels).
 template <int G, int WAVES, int DS>
-__global__ __launch_bounds__(64 * WAVES) void decode_merge_kernel(const pa_decode_params p) {
+__global__ __launch_bounds__(64 * WAVES) void decode_merge_kernel(const int32_t* __restrict__ isb,
+                                                                  const float* __restrict__ part_out,
+                                                                  const float* __restrict__ part_lse,
+                                                                  int num_kv_heads, const pa_decode_params p) {
     constexpr int LPS = DS / 4;      // lanes per segment
     constexpr int SPW = 64 / LPS;    // segments per wave per pass
     // The combine below exchanges lanes 4, 8, 16 and 32 apart only.
@@ -1220,10 +1226,10 @@ __global__ __launch_bounds__(64 * WAVES) void decode_merge_kernel(const pa_decod
     const int hqi  = blockIdx.x;
     const int b    = blockIdx.y;
     const int d0   = blockIdx.z * DS;
-    const int item = b * p.num_kv_heads + hqi / G;
+    const int item = b * num_kv_heads + hqi / G;
     const int g    = hqi % G;
-    const int s0 = p.item_seg_begin[item];
-    const int n  = p.item_seg_begin[item + 1] - s0;
+    const int s0 = isb[item];
+    const int n  = isb[item + 1] - s0;
     if (n <= 1) return;
 
     __shared__ float4 acc_lds[WAVES][LPS];
@@ -1243,8 +1249,8 @@ __global__ __launch_bounds__(64 * WAVES) void decode_merge_kernel(const pa_decod
 #pragma unroll 4
     for (int i = wave * SPW + sl; i < n; i += WAVES * SPW) {
         const size_t sg  = static_cast<size_t>(s0 + i);
-        const float  lse = p.partial_lse[sg * G + g];
-        const float4 o   = *reinterpret_cast<const float4*>(p.partial_out + (sg * G + g) * kHeadDim + d0 + 4 * dq);
+        const float  lse = part_lse[sg * G + g];
+        const float4 o   = *reinterpret_cast<const float4*>(part_out + (sg * G + g) * kHeadDim + d0 + 4 * dq);
         const float  mn  = fmaxf(m, lse);
         const float  f   = exp2_fast(m - mn);      // 0 while m = -inf
         const float  wgt = exp2_fast(lse - mn);
@@ -1392,9 +1398,11 @@ hipError_t launch_merge_gd(const pa_decode_params& p, hipStream_t s) {
     constexpr int SPW = 256 / DS;    // segments one wave covers per pass
     const int m = p.max_item_segments;
     if (m > 0 && m <= 4 * SPW)
-        hipLaunchKernelGGL((decode_merge_kernel<G, 1, DS>), grid, dim3(64), 0, s, p);
+        hipLaunchKernelGGL((decode_merge_kernel<G, 1, DS>), grid, dim3(64), 0, s, p.item_seg_begin, p.partial_out,
+                           p.partial_lse, p.num_kv_heads, p);
     else
-        hipLaunchKernelGGL((decode_merge_kernel<G, 4, DS>), grid, dim3(256), 0, s, p);
+        hipLaunchKernelGGL((decode_merge_kernel<G, 4, DS>), grid, dim3(256), 0, s, p.item_seg_begin, p.partial_out,
+                           p.partial_lse, p.num_kv_heads, p);
     return hipGetLastError();
 }
 
