@@ -78,7 +78,8 @@ typedef struct pa_decode_params {
     int32_t         max_item_segments; /* most segments of one (row, kv head); sizes the
                                           merge launch (0 = unknown). Set by bind. */
     int32_t         block_merge;       /* How the split kernel merges split (row, kv head)
-                                          items itself (needs_merge is then 0). Set by bind.
+                                          items itself (needs_merge is then 0; the launches
+                                          refuse both set). Set by bind.
                                           0: it does not (the merge kernel does, if
                                           needs_merge). 1: every split item lies in one
                                           block of 8 work units and is merged there in LDS.

@@ -1468,9 +1468,19 @@ int kernel_units_per_cu(int dtype, int group) {
     return std::max(1, std::min(blocks, tuned)) * kWaves;
 }
 
+// A plan's split rows are merged either by the merge kernel (needs_merge) or
+// inside the split kernel (block_merge), never both: with block_merge the
+// workspace holds partial rows only at the slots the split kernel merges
+// through, and the merge kernel would read the others unwritten.
+void check_merge_fields(const pa_decode_params& p) {
+    if (p.needs_merge && p.block_merge)
+        throw std::invalid_argument("decode: needs_merge and block_merge exclude each other (bind sets them)");
+}
+
 hipError_t launch_decode_split(int dtype, const pa_decode_params& p, hipStream_t s) {
     check_kv_dtype(dtype);
     const int g = checked_group(p);
+    check_merge_fields(p);
     if (p.num_ctas <= 0) return hipSuccess;
     if (p.page_size <= 0 || p.block_table_stride <= 0 || p.batch <= 0)
         throw std::invalid_argument("decode: page_size, block_table_stride and batch must be positive");
@@ -1488,6 +1498,7 @@ hipError_t launch_decode_split(int dtype, const pa_decode_params& p, hipStream_t
 hipError_t launch_decode_merge(int dtype, const pa_decode_params& p, hipStream_t s) {
     check_kv_dtype(dtype);
     const int g = checked_group(p);
+    check_merge_fields(p);
     if (!p.needs_merge || p.batch <= 0) return hipSuccess;
     if (!p.partial_out || !p.partial_lse || !p.item_seg_begin || !p.out)
         throw std::invalid_argument("decode merge: null pointer in params");

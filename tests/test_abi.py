@@ -56,6 +56,13 @@ def test_decode_rejects_bad_shapes_before_any_launch():
     p.num_q_heads = 32
     with pytest.raises(pa_amd.InvalidArgument):
         pa_amd.decode_split(pa_amd.FP16, p, 0)          # null pointers, page_size 0
+    # Split rows merged by the merge kernel and inside the split kernel at
+    # once: refused by both launches (the merge kernel would read partial
+    # slots the split kernel does not write).
+    p.needs_merge, p.block_merge = 1, 2
+    for launch in (pa_amd.decode_split, pa_amd.decode_merge, pa_amd.paged_decode):
+        with pytest.raises(pa_amd.InvalidArgument, match="exclude"):
+            launch(pa_amd.FP16, p, 0)
     lib = _lib.load()
     assert lib.pa_decode(0, None, None) == _lib.PA_ERR_INVALID_ARGUMENT
 
