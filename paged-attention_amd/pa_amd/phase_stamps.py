@@ -85,6 +85,9 @@ def stamps_of(s: Setup, steps: int = 200, flusher: Flusher | None = None) -> dic
     if lib.pa_debug_stamps(buf.ctypes.data, buf.nbytes) != 0:
         raise RuntimeError("pa_debug_stamps failed")
     st = buf.reshape(nb, SLOTS).astype(np.int64)
+    # A stamp older than its block's start belongs to an earlier step (a phase
+    # this step's block did not reach): dropped.
+    st = np.where(st >= st[:, :1], st, 0)
     t0 = st[:, 0].min()
 
     def us(x):
@@ -105,14 +108,13 @@ def stamps_of(s: Setup, steps: int = 200, flusher: Flusher | None = None) -> dic
          "xcd_mean_end": [round(float(cu_mean[x::8].mean()), 2) for x in range(8)] if nb % 8 == 0 else None}
     last_end = us(blk_end).max()
     if s.params.block_merge != 0:
-        ent = st[:, 16] > 0
-        cnt = np.maximum(st[:, 18], st[:, 19])
+        cnt = np.maximum(st[:, 18], st[:, 19])   # blocks holding a split segment
+        ent = (st[:, 16] > 0) & (cnt > 0)
         r["merge_barrier"] = p50_max((st[ent, 16] - blk_end[ent]) * TICK_US)
         r["merge_lds"] = p50_max((st[ent, 17] - st[ent, 16]) * TICK_US)
         r["merge_count"] = p50_max((cnt[ent] - st[ent, 17]) * TICK_US)
     if s.params.block_merge == 2:
         arr = st[:, 9] > 0
-        cnt = np.maximum(st[:, 18], st[:, 19])
         r["merge_average"] = p50_max((st[arr, 9] - cnt[arr]) * TICK_US)
         last = st[:, 15] > st[:, 11]
         r["merge_in_block"] = p50_max((st[arr, 9] - blk_end[arr]) * TICK_US)
