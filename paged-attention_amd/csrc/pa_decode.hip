@@ -158,6 +158,15 @@ __device__ __forceinline__ void stamp(int k) {
     (void)k;
 #endif
 }
+// The shader clock counter (s_memtime), for the CU's effective clock between
+// two stamps of the same wave.
+__device__ __forceinline__ void stamp_clock(int k) {
+#if PA_STAMPS
+    if ((threadIdx.x & 63) == 0 && blockIdx.x < 4096) pa_stamps[blockIdx.x * 24 + k] = __builtin_amdgcn_s_memtime();
+#else
+    (void)k;
+#endif
+}
 
 namespace pa {
 namespace {
@@ -579,7 +588,10 @@ __device__ __forceinline__ void decode_split_body(const pa_decode_params& p, con
     __shared__ __attribute__((aligned(16))) float part_lds[2 * kWaves][G * kHeadDim];
     __shared__ float lse_lds[2 * kWaves][G];
 
-    if (threadIdx.x == 0) stamp(0);
+    if (threadIdx.x == 0) {
+        stamp(0);
+        stamp_clock(20);
+    }
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lblock = static_cast<int>(blockIdx.x);   // units 8 lblock .. 8 lblock + 7
@@ -1166,6 +1178,7 @@ __device__ __forceinline__ void decode_split_body(const pa_decode_params& p, con
     }
     }   // seg_begin < seg_end
     stamp(1 + wave);
+    if (wave == 0) stamp_clock(21);
 
     if (merge_here) {
         __syncthreads();

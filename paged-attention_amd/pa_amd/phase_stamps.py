@@ -17,6 +17,8 @@ One JSON line per shape:
   wave_end           p0 / p50 / p100 of the waves' ends of their split loop
   block_mean_end     p0 / p50 / p100 over blocks of their waves' mean end
   xcd_mean_end       that mean per XCD (blocks b, b + 8, ... run on XCD b % 8)
+  xcd_clock_mhz      the shader clock per XCD over wave 0's split loop (s_memtime
+                     ticks per microsecond)
   merge_in_block     per block, from its last wave's end to its merged items
                      (the LDS merge, and for items that span blocks the
                      partial row stored), then its parts: barrier (to the
@@ -45,7 +47,8 @@ from . import core
 from .bench_decode import Flusher, Setup
 
 TICK_US = 0.01   # s_memrealtime runs at 100 MHz
-SLOTS = 24       # stamps per block: 0 start, 1-8 wave ends, 9-15 and 16-19 the merge phases
+SLOTS = 24       # stamps per block: 0 start, 1-8 wave ends, 9-15 and 16-19 the merge phases,
+                 # 20-21 the shader clock (s_memtime) at the start and at wave 0's end
 
 
 def stamps_of(s: Setup, steps: int = 200, flusher: Flusher | None = None) -> dict:
@@ -85,6 +88,8 @@ def stamps_of(s: Setup, steps: int = 200, flusher: Flusher | None = None) -> dic
     if lib.pa_debug_stamps(buf.ctypes.data, buf.nbytes) != 0:
         raise RuntimeError("pa_debug_stamps failed")
     st = buf.reshape(nb, SLOTS).astype(np.int64)
+    clk = st[:, 20:22].copy()      # another counter: not comparable with the 100 MHz stamps
+    st[:, 20:22] = 0
     # A stamp older than its block's start belongs to an earlier step (a phase
     # this step's block did not reach): dropped.
     st = np.where(st >= st[:, :1], st, 0)
@@ -106,6 +111,12 @@ def stamps_of(s: Setup, steps: int = 200, flusher: Flusher | None = None) -> dic
          "wave_end": [round(float(np.percentile(us(wend), q)), 2) for q in (0, 50, 100)],
          "block_mean_end": [round(float(np.percentile(cu_mean, q)), 2) for q in (0, 50, 100)],
          "xcd_mean_end": [round(float(cu_mean[x::8].mean()), 2) for x in range(8)] if nb % 8 == 0 else None}
+    # Shader clock of each block's CU over wave 0's split loop (MHz).
+    span = (st[:, 1] - st[:, 0]) * TICK_US
+    ok = (span > 0) & (clk[:, 1] > clk[:, 0])
+    mhz = np.where(ok, (clk[:, 1] - clk[:, 0]) / np.where(span > 0, span, 1), np.nan)
+    if nb % 8 == 0 and ok.any():
+        r["xcd_clock_mhz"] = [round(float(np.nanmean(mhz[x::8])), 0) for x in range(8)]
     last_end = us(blk_end).max()
     if s.params.block_merge != 0:
         cnt = np.maximum(st[:, 18], st[:, 19])   # blocks holding a split segment
