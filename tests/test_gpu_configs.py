@@ -34,6 +34,21 @@ def test_decoder_full_size_config2():
     err, _ = decoder_case(32, [8192] * 32, False, threads=16)
     assert err < TOL, err
 
+@pytest.mark.parametrize("batch,length,hq,hkv,fp8", [
+    (32, 8192, 4, 1, False),     # C2 sharded over 8 GPUs by kv head: one GPU's share
+    (4, 8192, 32, 8, False),     # C2 sharded by row
+    (64, 8192, 4, 1, True),      # C3 sharded by kv head
+    (1, 16384, 32, 8, True),     # C5 FP8 sharded by tokens (one eighth of the sequence)
+], ids=["c2_heads8", "c2_rows8", "c3_heads8", "c5fp8_tokens8"])
+def test_decoder_shard_shapes(batch, length, hq, hkv, fp8):
+    """One GPU's share of an 8-way sharded BASELINE step at its real shape
+    (the shapes the sharding design is timed at), against the oracle: rows
+    cut over 4 or 8 blocks and merged across them in the split kernel, or
+    over 32 blocks and merged by the merge kernel."""
+    err, dec = decoder_case(batch, [length] * batch, fp8, hq=hq, hkv=hkv, threads=16)
+    assert dec.num_segments > batch * hkv   # split rows
+    assert err < TOL, err
+
 def test_decoder_full_size_config3():
     """Config C3 at full size: 64 x 8192, FP8 E4M3 (amax/448 scales,
     quantized by the append kernel), 16-token scattered pages."""
