@@ -49,6 +49,16 @@ def test_decoder_shard_shapes(batch, length, hq, hkv, fp8):
     assert dec.num_segments > batch * hkv   # split rows
     assert err < TOL, err
 
+@pytest.mark.parametrize("hq", [8, 16, 64], ids=["g1", "g2", "g8"])
+@pytest.mark.parametrize("fp8", [False, True], ids=["fp16", "fp8"])
+def test_decoder_full_size_gqa_groups(hq, fp8):
+    """C2's batch and length (32 x 8192, 8 kv heads, 16-token scattered
+    pages) with the other GQA groups (1, 2, 8 query heads per kv head; C2
+    itself is 4), fp16 and FP8, against the oracle: the shapes timed beside
+    C2 for the group sweep."""
+    err, _ = decoder_case(32, [8192] * 32, fp8, hq=hq, hkv=8, threads=16)
+    assert err < TOL, err
+
 def test_decoder_full_size_config3():
     """Config C3 at full size: 64 x 8192, FP8 E4M3 (amax/448 scales,
     quantized by the append kernel), 16-token scattered pages."""
