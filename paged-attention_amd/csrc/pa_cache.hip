@@ -97,7 +97,7 @@ __device__ __forceinline__ u32x2 encode8_hw(const u32x4 in, float inv) {
 }
 
 // E4M3 bytes of eight products float(x) * inv, in software (e4m3_encode).
-__device__ __forceinline__ u32x2 encode8_sw(const u32x4 in, float inv) {
+[[maybe_unused]] __device__ __forceinline__ u32x2 encode8_sw(const u32x4 in, float inv) {
     u32x2 out = {0u, 0u};
 #pragma unroll
     for (int e = 0; e < 8; ++e)
